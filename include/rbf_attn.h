@@ -1,0 +1,134 @@
+/*
+ * rbf_attn.h - C ABI of the MI355X (gfx950) fused RBF attention library
+ * (librbfattn.so).
+ *
+ * RBF attention scores a query/key pair by -gamma * ||q_i - k_j||^2.
+ * Softmax variant:   O = softmax_j(2*gamma*q.k - gamma*||k||^2) V, and the
+ *                    row log-sum-exp L is kept in base 2 (log2 of the
+ *                    normaliser of exp2(log2(e) * logits)).
+ * Non-softmax:       O_i = sum_j exp(-gamma*||q_i - k_j||^2) v_j
+ *                    (no max, no normaliser, no L).
+ *
+ * Every entry point below replaces one piece of the reference's launch code
+ * in rbf_attention.py (4rtemi5/rbf_attention); the host side is the
+ * torch.library custom-op layer in rbf_attention_amd/ops.py, which keeps the
+ * reference op names and schemas.
+ *
+ * Conventions
+ *  - Tensors are (B, H, N, D) with arbitrary strides on B, H and N (in
+ *    elements) and unit stride on D.  Base pointers must be 16-byte aligned
+ *    and every stride a multiple of 16 bytes; violations return
+ *    RBF_ATTN_EINVAL_STRIDE and launch nothing.
+ *  - lse and delta are fp32, contiguous (B, H, N).
+ *  - The library never allocates device memory: outputs and the fp32
+ *    workspaces are owned by the caller.
+ *  - All kernels are enqueued on the caller's stream (hipStream_t passed as
+ *    void*; NULL = legacy default stream).  Calls never synchronise.
+ *  - Calls are re-entrant; the last error message is thread-local.
+ *  - Return value 0 = success, negative = error code below.
+ */
+#ifndef RBF_ATTN_H_
+#define RBF_ATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RBF_ATTN_ABI_VERSION 1
+
+/* variant */
+#define RBF_ATTN_SOFTMAX 0
+#define RBF_ATTN_NON_SOFTMAX 1
+
+/* dtype */
+#define RBF_ATTN_BF16 0
+#define RBF_ATTN_FP16 1
+#define RBF_ATTN_FP32 2
+
+/* error codes */
+#define RBF_ATTN_OK 0
+#define RBF_ATTN_EINVAL_ARGS -1    /* null args, bad abi version, bad enum  */
+#define RBF_ATTN_EINVAL_DTYPE -2   /* unknown dtype                         */
+#define RBF_ATTN_EINVAL_STRIDE -3  /* misaligned pointer or stride          */
+#define RBF_ATTN_EINVAL_HEADDIM -4 /* D outside [8, 128] or D % 8 != 0      */
+#define RBF_ATTN_EINVAL_SHAPE -5   /* negative sizes, grid too large        */
+#define RBF_ATTN_EINVAL_PTR -6     /* a required pointer is NULL            */
+#define RBF_ATTN_ELAUNCH -7        /* the HIP runtime rejected a launch     */
+
+/* One (B, H, N, D) operand: base pointer and element strides of dims 0-2. */
+typedef struct rbf_attn_tensor {
+  void* ptr;
+  int64_t stride_b;
+  int64_t stride_h;
+  int64_t stride_n;
+} rbf_attn_tensor;
+
+typedef struct rbf_attn_args {
+  int32_t abi_version; /* must be RBF_ATTN_ABI_VERSION                       */
+  int32_t variant;     /* RBF_ATTN_SOFTMAX | RBF_ATTN_NON_SOFTMAX            */
+  int32_t dtype;       /* element type shared by q,k,v,o,dout,dq,dk,dv       */
+  int32_t B, H, N, D;
+  int32_t causal;      /* 1: key j visible to query i iff j <= i             */
+  int32_t num_prefix;  /* keys j < num_prefix are visible to every query
+                          (register tokens); 0 = plain causal mask          */
+  float gamma;         /* RBF bandwidth; the reference's sm_scale = 1/sqrt(D) */
+  rbf_attn_tensor q, k, v;
+  rbf_attn_tensor o;    /* fwd: written; bwd (softmax): read for Delta      */
+  rbf_attn_tensor dout; /* bwd: read                                          */
+  rbf_attn_tensor dq, dk, dv; /* bwd: written                               */
+  float* lse;   /* softmax fwd: written (base-2 LSE); softmax bwd: read.
+                   non-softmax bwd: fp32 (B,H,N) workspace, overwritten.    */
+  float* delta; /* softmax bwd: fp32 (B,H,N) workspace, overwritten with
+                   rowsum(O*dO).  Unused (may be NULL) for non-softmax.     */
+} rbf_attn_args;
+
+/*
+ * Forward pass: writes o (and lse for the softmax variant).
+ * Replaces the Triton launches of
+ *   rbf_scaled_fwd       rbf_attention.py:651-690 (_rbf_attn_fwd_kernel,
+ *                        rbf_attention.py:65-219), and
+ *   rbf_non_softmax_fwd  rbf_attention.py:1355-1391
+ *                        (_rbf_non_softmax_fwd_kernel, rbf_attention.py:861-997).
+ * Two kernels' worth of launch code collapse into one call: variant selects.
+ */
+int rbf_attn_fwd(const rbf_attn_args* args, void* stream);
+
+/*
+ * Backward pass: writes dq, dk, dv (and the lse/delta workspaces as noted).
+ * Replaces the Triton launches of
+ *   rbf_scaled_bwd       rbf_attention.py:702-810 (_bwd_preprocess 222-276,
+ *                        _rbf_attn_bwd_dk_dv_kernel 279-477,
+ *                        _rbf_attn_bwd_dq_kernel 480-642), and
+ *   rbf_non_softmax_bwd  rbf_attention.py:1399-1480
+ *                        (_rbf_non_softmax_bwd_dk_dv_kernel 1000-1184,
+ *                        _rbf_non_softmax_bwd_dq_kernel 1187-1352).
+ * Two launches on the stream: the dQ kernel (which also produces Delta, or
+ * for the non-softmax variant the per-query norm offsets) and then the
+ * dK/dV kernel that consumes them.
+ */
+int rbf_attn_bwd(const rbf_attn_args* args, void* stream);
+
+/*
+ * One stage of rbf_attn_bwd: stage 1 = the dQ kernel (also writes Delta, or
+ * the non-softmax norm offsets, into the workspaces), stage 2 = the dK/dV
+ * kernel (reads them).  rbf_attn_bwd == stage 1 then stage 2 on one stream.
+ * No reference counterpart: it exists so callers can time or schedule the
+ * two kernels separately.  Same validation and error codes as rbf_attn_bwd;
+ * any other stage value returns RBF_ATTN_EINVAL_ARGS.
+ */
+int rbf_attn_bwd_stage(const rbf_attn_args* args, void* stream, int stage);
+
+/* Message describing the last failed call on this thread ("" if none).
+ * No reference counterpart: the reference surfaces Triton exceptions. */
+const char* rbf_attn_last_error(void);
+
+/* RBF_ATTN_ABI_VERSION of the loaded library. No reference counterpart. */
+int rbf_attn_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RBF_ATTN_H_ */

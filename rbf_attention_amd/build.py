@@ -1,0 +1,81 @@
+"""Build librbfattn.so (HIP kernels for gfx950 + the C ABI) in-tree.
+
+Usage:  python -m rbf_attention_amd.build      (or build() from Python)
+
+The library lands next to this file, so it travels with the source tree.
+Each element type's kernels are a separate translation unit, compiled in
+parallel, then linked with the C ABI into one shared object.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+CSRC = os.path.join(PKG_DIR, "csrc")
+INCLUDE = os.path.join(REPO_DIR, "include")
+LIB_NAME = "librbfattn.so"
+LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+ARCH = os.environ.get("RBF_ATTN_ARCH", "gfx950")
+
+# Packed-FP32 VALU ops are disabled for all device code.
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INCLUDE}",
+    f"-I{CSRC}",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in proc.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+
+
+def build(verbose: bool = True) -> str:
+    """Compile every HIP translation unit for gfx950 and link librbfattn.so."""
+    hipcc = _hipcc()
+    units = [
+        ("rbf_attn_capi.hip", []),
+        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=0"]),
+        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=1"]),
+        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=2"]),
+    ]
+    with tempfile.TemporaryDirectory(prefix="rbfattn_build_") as tmp:
+        jobs = []
+        for idx, (src, extra) in enumerate(units):
+            obj = os.path.join(tmp, f"u{idx}.o")
+            cmd = [hipcc, *COMMON_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
+            jobs.append((cmd, obj))
+        workers = min(len(jobs), max(1, min(16, os.cpu_count() or 1)))
+        with cf.ThreadPoolExecutor(workers) as ex:
+            list(ex.map(lambda j: _run(j[0]), jobs))
+        tmp_lib = os.path.join(tmp, LIB_NAME)
+        _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp_lib, *[o for _, o in jobs]])
+        shutil.copyfile(tmp_lib, LIB_PATH + ".tmp")
+        os.replace(LIB_PATH + ".tmp", LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}", file=sys.stderr)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build()

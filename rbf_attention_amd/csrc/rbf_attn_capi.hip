@@ -1,0 +1,197 @@
+// C ABI of librbfattn.so: argument validation, parameter packing and dispatch
+// to the per-dtype launchers.  Nothing here allocates device memory or
+// synchronises; every error is detected before the first launch.
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <hip/hip_runtime.h>
+
+#include "rbf_attn.h"
+#include "rbf_attn_kernels.h"
+#include "rbf_attn_launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+size_t elem_size(int dtype) { return dtype == RBF_ATTN_FP32 ? 4 : 2; }
+
+int check_tensor(const char* name, const rbf_attn_tensor& t, size_t esz) {
+  if (t.ptr == nullptr) return fail(RBF_ATTN_EINVAL_PTR, "%s: null pointer", name);
+  if (reinterpret_cast<uintptr_t>(t.ptr) % 16 != 0)
+    return fail(RBF_ATTN_EINVAL_STRIDE, "%s: base pointer not 16-byte aligned", name);
+  const int64_t s[3] = {t.stride_b, t.stride_h, t.stride_n};
+  for (int i = 0; i < 3; ++i)
+    if ((s[i] * (int64_t)esz) % 16 != 0)
+      return fail(RBF_ATTN_EINVAL_STRIDE, "%s: stride %d (%lld elements) is not a multiple of 16 bytes", name, i,
+                  (long long)s[i]);
+  return RBF_ATTN_OK;
+}
+
+int check_common(const rbf_attn_args* a) {
+  g_err[0] = '\0';
+  if (a == nullptr) return fail(RBF_ATTN_EINVAL_ARGS, "args is NULL");
+  if (a->abi_version != RBF_ATTN_ABI_VERSION)
+    return fail(RBF_ATTN_EINVAL_ARGS, "abi_version %d != library %d", a->abi_version, RBF_ATTN_ABI_VERSION);
+  if (a->variant != RBF_ATTN_SOFTMAX && a->variant != RBF_ATTN_NON_SOFTMAX)
+    return fail(RBF_ATTN_EINVAL_ARGS, "unknown variant %d", a->variant);
+  if (a->dtype != RBF_ATTN_BF16 && a->dtype != RBF_ATTN_FP16 && a->dtype != RBF_ATTN_FP32)
+    return fail(RBF_ATTN_EINVAL_DTYPE, "unknown dtype %d", a->dtype);
+  if (a->B < 0 || a->H < 0 || a->N < 0)
+    return fail(RBF_ATTN_EINVAL_SHAPE, "negative size B=%d H=%d N=%d", a->B, a->H, a->N);
+  if (a->D < 8 || a->D > 128 || a->D % 8 != 0)
+    return fail(RBF_ATTN_EINVAL_HEADDIM, "head dim D=%d unsupported (need 8 <= D <= 128, D %% 8 == 0)", a->D);
+  if (a->causal != 0 && a->causal != 1) return fail(RBF_ATTN_EINVAL_ARGS, "causal must be 0 or 1");
+  if (a->num_prefix < 0) return fail(RBF_ATTN_EINVAL_ARGS, "num_prefix must be >= 0");
+  if (!(a->gamma > 0.f) || !isfinite(a->gamma))
+    return fail(RBF_ATTN_EINVAL_ARGS, "gamma must be finite and > 0 (got %g)", (double)a->gamma);
+  // Token indices and the grid are 32-bit.
+  if (a->N > (1 << 30)) return fail(RBF_ATTN_EINVAL_SHAPE, "N=%d too large", a->N);
+  const long long nblk = (a->N + 31) / 32;
+  const long long grid = (long long)a->B * a->H * ((nblk + 3) / 4);
+  if (grid > 0x7fffffffLL) return fail(RBF_ATTN_EINVAL_SHAPE, "grid of %lld work-groups too large", grid);
+  if ((long long)a->B * a->H * a->N > (1LL << 40)) return fail(RBF_ATTN_EINVAL_SHAPE, "B*H*N too large");
+  return RBF_ATTN_OK;
+}
+
+int check_f32(const char* name, const float* p) {
+  if (p == nullptr) return fail(RBF_ATTN_EINVAL_PTR, "%s: null pointer", name);
+  if (reinterpret_cast<uintptr_t>(p) % 4 != 0) return fail(RBF_ATTN_EINVAL_STRIDE, "%s: not 4-byte aligned", name);
+  return RBF_ATTN_OK;
+}
+
+void copy_strides(int64_t dst[3], const rbf_attn_tensor& t) {
+  dst[0] = t.stride_b;
+  dst[1] = t.stride_h;
+  dst[2] = t.stride_n;
+}
+
+rbf::Params make_params(const rbf_attn_args* a) {
+  rbf::Params p = {};
+  p.q = a->q.ptr;
+  p.k = a->k.ptr;
+  p.v = a->v.ptr;
+  p.o = a->o.ptr;
+  p.dout = a->dout.ptr;
+  p.dq = a->dq.ptr;
+  p.dk = a->dk.ptr;
+  p.dv = a->dv.ptr;
+  p.lse = a->lse;
+  p.delta = a->delta;
+  copy_strides(p.sq, a->q);
+  copy_strides(p.sk, a->k);
+  copy_strides(p.sv, a->v);
+  copy_strides(p.so, a->o);
+  copy_strides(p.sdo, a->dout);
+  copy_strides(p.sdq, a->dq);
+  copy_strides(p.sdk, a->dk);
+  copy_strides(p.sdv, a->dv);
+  p.B = a->B;
+  p.H = a->H;
+  p.N = a->N;
+  p.D = a->D;
+  p.causal = a->causal;
+  p.num_prefix = a->num_prefix;
+  p.gamma = a->gamma;
+  p.c = (float)(2.0 * (double)a->gamma * 1.4426950408889634);
+  const int rem = a->N % 32;
+  p.org = rem == 0 ? 0 : rem - 32;
+  p.nblk = (a->N - p.org) / 32;
+  return p;
+}
+
+int launched(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(RBF_ATTN_ELAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+  return RBF_ATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rbf_attn_abi_version(void) { return RBF_ATTN_ABI_VERSION; }
+
+const char* rbf_attn_last_error(void) { return g_err; }
+
+int rbf_attn_fwd(const rbf_attn_args* a, void* stream) {
+  int rc = check_common(a);
+  if (rc) return rc;
+  const size_t esz = elem_size(a->dtype);
+  if ((rc = check_tensor("q", a->q, esz))) return rc;
+  if ((rc = check_tensor("k", a->k, esz))) return rc;
+  if ((rc = check_tensor("v", a->v, esz))) return rc;
+  if ((rc = check_tensor("o", a->o, esz))) return rc;
+  if (a->variant == RBF_ATTN_SOFTMAX && (rc = check_f32("lse", a->lse))) return rc;
+  if ((long long)a->B * a->H * a->N == 0) return RBF_ATTN_OK;
+  const rbf::Params p = make_params(a);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (a->dtype) {
+    case RBF_ATTN_BF16: e = rbf::launch_fwd_bf16(p, a->variant, st); break;
+    case RBF_ATTN_FP16: e = rbf::launch_fwd_fp16(p, a->variant, st); break;
+    default: e = rbf::launch_fwd_fp32(p, a->variant, st); break;
+  }
+  return launched(e, "forward");
+}
+
+static int bwd_impl(const rbf_attn_args* a, void* stream, int stage) {
+  int rc = check_common(a);
+  if (rc) return rc;
+  if (stage < 0 || stage > 2) return fail(RBF_ATTN_EINVAL_ARGS, "unknown backward stage %d", stage);
+  const size_t esz = elem_size(a->dtype);
+  if ((rc = check_tensor("q", a->q, esz))) return rc;
+  if ((rc = check_tensor("k", a->k, esz))) return rc;
+  if ((rc = check_tensor("v", a->v, esz))) return rc;
+  if ((rc = check_tensor("dout", a->dout, esz))) return rc;
+  if ((rc = check_tensor("dq", a->dq, esz))) return rc;
+  if ((rc = check_tensor("dk", a->dk, esz))) return rc;
+  if ((rc = check_tensor("dv", a->dv, esz))) return rc;
+  if ((rc = check_f32("lse", a->lse))) return rc;
+  if (a->variant == RBF_ATTN_SOFTMAX) {
+    if ((rc = check_tensor("o", a->o, esz))) return rc;
+    if ((rc = check_f32("delta", a->delta))) return rc;
+  }
+  if ((long long)a->B * a->H * a->N == 0) return RBF_ATTN_OK;
+  const rbf::Params p = make_params(a);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (stage == 0 || stage == 1) {
+    switch (a->dtype) {
+      case RBF_ATTN_BF16: e = rbf::launch_bwd_dq_bf16(p, a->variant, st); break;
+      case RBF_ATTN_FP16: e = rbf::launch_bwd_dq_fp16(p, a->variant, st); break;
+      default: e = rbf::launch_bwd_dq_fp32(p, a->variant, st); break;
+    }
+    if ((rc = launched(e, "backward dQ"))) return rc;
+  }
+  if (stage == 0 || stage == 2) {
+    switch (a->dtype) {
+      case RBF_ATTN_BF16: e = rbf::launch_bwd_dkdv_bf16(p, a->variant, st); break;
+      case RBF_ATTN_FP16: e = rbf::launch_bwd_dkdv_fp16(p, a->variant, st); break;
+      default: e = rbf::launch_bwd_dkdv_fp32(p, a->variant, st); break;
+    }
+    if ((rc = launched(e, "backward dK/dV"))) return rc;
+  }
+  return RBF_ATTN_OK;
+}
+
+int rbf_attn_bwd(const rbf_attn_args* a, void* stream) { return bwd_impl(a, stream, 0); }
+
+int rbf_attn_bwd_stage(const rbf_attn_args* a, void* stream, int stage) {
+  if (stage != 1 && stage != 2) {
+    g_err[0] = '\0';
+    return fail(RBF_ATTN_EINVAL_ARGS, "unknown backward stage %d", stage);
+  }
+  return bwd_impl(a, stream, stage);
+}
+
+}  // extern "C"

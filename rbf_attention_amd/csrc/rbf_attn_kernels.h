@@ -1,0 +1,834 @@
+// Fused RBF attention kernels for MI355X (gfx950, CDNA4).
+//
+// Math (reference: rbf_attention.py:65-219, 279-642, 861-1352):
+//   acc_ij = q_i.k_j - 0.5*||k_j||^2               (MFMA, fp32 accumulate)
+//   softmax:     P_ij = exp2(c*acc_ij - L_i),  c = 2*gamma*log2(e)
+//                L_i  = base-2 log-sum-exp of c*acc_i.  (rbf_attention.py:219)
+//   non-softmax: P_ij = exp2(c*acc_ij - c*0.5*||q_i||^2) = exp(-gamma||q_i-k_j||^2)
+//   bwd: dP = dO.V^T; dS = P*(dP - Delta) (softmax) or P*dP (non-softmax)
+//        dV = P^T dO; dQ = 2g(dS.K - rowsum(dS) q) [rowsum term non-softmax only]
+//        dK = 2g(dS^T.Q - colsum(dS) k)
+//
+// Layout choices (all MFMA are v_mfma_f32_32x32x16_{bf16,f16}, or eight
+// v_mfma_f32_32x32x2f32 for fp32):
+//  * A 32x32 MFMA accumulator holds, in lane l = 32h + n, column n and the 16
+//    rows crow(i, h) = 8(i/4) + 4h + (i%4).  Every product is oriented so that
+//    the column index is the token the wave "owns" (the query in fwd/dQ, the
+//    key in dK/dV): softmax statistics, L, Delta, the key norm and the
+//    row/column sums are then per-lane scalars.
+//  * An operand fragment is 8 elements per lane: lane (n, h), k-step t holds
+//    contraction indices 16t + 8h + s (s = 0..7).  Both operands of one MFMA
+//    use the same convention, so any hardware K-order is consistent.
+//  * An accumulator reused as an operand (P, dS) contributes contraction index
+//    crow(8t + s, h) = 16t + 8(s/4) + 4h + s%4 at slot s of k-step t.  The
+//    other operand is read from a "transposed" LDS tile whose token axis is
+//    stored in permuted order swap23(r) (bits 2 and 3 of the token index
+//    swapped), which turns that index set back into 8 contiguous elements.
+//  * Token axis is cut into 32-token blocks aligned to the END of the
+//    sequence: block b covers [org + 32b, org + 32b + 32), org = -(-N mod 32).
+//    The ragged part (e.g. 4 register tokens of N = 516) is the head of
+//    block 0, which causal attention touches least.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rbf {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x8_t __attribute__((ext_vector_type(8)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+// Lazy rescale threshold (base-2 units): the running max is only raised when a
+// new tile exceeds it by more than this, so P <= 2^kTau before normalising.
+constexpr float kTau = 8.0f;
+
+// Kernel parameters, shared by all kernels (passed by value).
+struct Params {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;     // fwd: output (written); bwd softmax: read for Delta
+  const void* dout;
+  void* dq;
+  void* dk;
+  void* dv;
+  float* lse;        // (B,H,N) fp32
+  float* delta;      // (B,H,N) fp32
+  int64_t sq[3], sk[3], sv[3], so[3], sdo[3], sdq[3], sdk[3], sdv[3];
+  int B, H, N, D;
+  int causal, num_prefix;
+  float gamma;       // RBF bandwidth
+  float c;           // 2 * gamma * log2(e)
+  int org;           // first token of block 0 (<= 0)
+  int nblk;          // number of 32-token blocks
+};
+
+// ---------------------------------------------------------------------------
+// Element traits: fragment type, MFMA, LDS padding.
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<__bf16> {
+  typedef bf16x8_t frag;
+  typedef bf16x4_t quad;
+  typedef u32x4_t raw;
+  static constexpr int PAD = 8;  // 16 bytes
+  __device__ static inline f32x16_t mma(frag a, frag b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Elem<_Float16> {
+  typedef f16x8_t frag;
+  typedef f16x4_t quad;
+  typedef u32x4_t raw;
+  static constexpr int PAD = 8;
+  __device__ static inline f32x16_t mma(frag a, frag b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Elem<float> {
+  typedef f32x8_t frag;
+  typedef f32x4_t quad;
+  typedef u32x8_t raw;
+  static constexpr int PAD = 4;  // 16 bytes
+  __device__ static inline f32x16_t mma(frag a, frag b, f32x16_t c) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[s], c, 0, 0, 0);
+    return c;
+  }
+};
+
+template <typename T>
+__device__ inline typename Elem<T>::frag zero_frag() {
+  typedef typename Elem<T>::raw raw;
+  raw z = {};
+  return __builtin_bit_cast(typename Elem<T>::frag, z);
+}
+
+// 8 consecutive elements; p is 16-byte aligned.
+template <typename T>
+__device__ inline typename Elem<T>::frag ld8(const T* p) {
+  typedef typename Elem<T>::raw raw;
+  typedef raw raw16 __attribute__((aligned(16)));
+  return __builtin_bit_cast(typename Elem<T>::frag, *reinterpret_cast<const raw16*>(p));
+}
+
+template <typename T>
+__device__ inline void st8(T* p, typename Elem<T>::frag f) {
+  typedef typename Elem<T>::raw raw;
+  typedef raw raw16 __attribute__((aligned(16)));
+  *reinterpret_cast<raw16*>(p) = __builtin_bit_cast(raw, f);
+}
+
+// 4 consecutive elements (8-byte aligned for 16-bit types, 16 for fp32).
+template <typename T>
+__device__ inline void ld4f(const T* p, float out[4]) {
+  typedef typename Elem<T>::quad quad;
+  typedef quad quadA __attribute__((aligned(sizeof(T) * 4)));
+  quad v = *reinterpret_cast<const quadA*>(p);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) out[e] = (float)v[e];
+}
+
+template <typename T>
+__device__ inline void st4f(T* p, const float in[4]) {
+  typedef typename Elem<T>::quad quad;
+  typedef quad quadA __attribute__((aligned(sizeof(T) * 4)));
+  quad v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = (T)in[e];
+  *reinterpret_cast<quadA*>(p) = v;
+}
+
+__device__ inline int swap23(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+// Row of accumulator element i held by lane half h (32x32 MFMA C layout).
+__device__ inline int crow(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ inline f32x16_t zero16() {
+  f32x16_t z = {};
+  return z;
+}
+
+template <typename T>
+__device__ inline float sumsq8(typename Elem<T>::frag f) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float x = (float)f[e];
+    s = fmaf(x, x, s);
+  }
+  return s;
+}
+
+template <typename T>
+__device__ inline float dot8(typename Elem<T>::frag a, typename Elem<T>::frag b) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s = fmaf((float)a[e], (float)b[e], s);
+  return s;
+}
+
+template <typename T>
+__device__ inline uint32_t bits16(T x) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, x);
+}
+
+// ---------------------------------------------------------------------------
+// Cooperative tile of ROWS tokens x DP features, staged global -> registers
+// -> LDS.  Work unit = two adjacent rows x 8 features.  Consecutive threads
+// take consecutive 8-feature chunks of a row pair, so each load instruction
+// reads whole rows.
+// ---------------------------------------------------------------------------
+template <typename T, int ROWS, int DP, int NT>
+struct Tile {
+  typedef typename Elem<T>::frag frag;
+  static constexpr int CPR = DP / 8;
+  static constexpr int UNITS = (ROWS / 2) * CPR;
+  static constexpr int PER = (UNITS + NT - 1) / NT;
+  static_assert(NT % CPR == 0, "a row pair must not straddle threads unevenly");
+  frag r[PER][2];
+
+  __device__ inline void load(const T* base, int64_t sn, int tok0, int N, int D, int tid) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int u = tid + j * NT;
+      const int rp = u / CPR, dc = u % CPR;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int tok = tok0 + 2 * rp + e;
+        if (u < UNITS && tok >= 0 && tok < N && dc * 8 < D)
+          r[j][e] = ld8<T>(base + (int64_t)tok * sn + dc * 8);
+        else
+          r[j][e] = zero_frag<T>();
+      }
+    }
+  }
+
+  // lds[row * LD + feature]
+  template <int LD>
+  __device__ inline void store_rows(T* lds, int tid) const {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int u = tid + j * NT;
+      if (UNITS % NT != 0 && u >= UNITS) continue;
+      const int rp = u / CPR, dc = u % CPR;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) st8<T>(lds + (2 * rp + e) * LD + dc * 8, r[j][e]);
+    }
+  }
+
+  // lds[feature * LDT + swap23(row)]
+  template <int LDT>
+  __device__ inline void store_trans(T* lds, int tid) const {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int u = tid + j * NT;
+      if (UNITS % NT != 0 && u >= UNITS) continue;
+      const int rp = u / CPR, dc = u % CPR;
+      const int pos = swap23(2 * rp);  // even; row 2rp+1 lands at pos+1
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const uint32_t w = bits16<T>(r[j][0][c]) | (bits16<T>(r[j][1][c]) << 16);
+          *reinterpret_cast<uint32_t*>(lds + (dc * 8 + c) * LDT + pos) = w;
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          lds[(dc * 8 + c) * LDT + pos] = r[j][0][c];
+          lds[(dc * 8 + c) * LDT + pos + 1] = r[j][1][c];
+        }
+      }
+    }
+  }
+
+  // nrm[row] = 0.5 * ||row||^2 in fp32 (from the input-dtype values).
+  __device__ inline void store_halfnorm(float* nrm, int tid) const {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int u = tid + j * NT;
+      const int rp = u / CPR, dc = u % CPR;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        float s = sumsq8<T>(r[j][e]);
+#pragma unroll
+        for (int m = 1; m < CPR; m <<= 1) s += __shfl_xor(s, m);
+        if (dc == 0 && u < UNITS) nrm[2 * rp + e] = 0.5f * s;
+      }
+    }
+  }
+};
+
+// Work-group -> (b*H + h, group) with an XCD-aware remap: the hardware deals
+// work-groups round-robin over the 8 XCDs, so consecutive logical indices
+// (the groups of one head, which share K/V or Q/dO) are packed onto the same
+// XCD to share its L2.
+__device__ inline void decode_wg(int ngrp, bool reverse, int& bh, int& grp) {
+  const int total = gridDim.x;
+  const int bid = blockIdx.x;
+  int L = bid;
+  if ((total & 7) == 0) L = (bid & 7) * (total >> 3) + (bid >> 3);
+  bh = L / ngrp;
+  const int j = L - bh * ngrp;
+  grp = reverse ? (ngrp - 1 - j) : j;
+}
+
+// ---------------------------------------------------------------------------
+// Forward.  One wave owns 32 queries (one block); a work-group owns W
+// consecutive blocks and streams BN-key tiles of K (row-major) and V
+// (transposed) through double-buffered LDS.  O^T = V^T . P^T on MFMA.
+// ---------------------------------------------------------------------------
+template <typename T, int DP, int W, int BN, bool SOFTMAX>
+__global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
+  typedef Elem<T> E;
+  typedef typename E::frag frag;
+  constexpr int NT = 64 * W, KB = BN / 32, KS = DP / 16, ND = DP / 32;
+  constexpr int LDR = DP + E::PAD, LDT = BN + E::PAD;
+  __shared__ __attribute__((aligned(16))) T sK[2][BN * LDR];
+  __shared__ __attribute__((aligned(16))) T sVt[2][DP * LDT];
+  __shared__ __attribute__((aligned(16))) float sKn[2][BN];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int N = p.N, D = p.D, org = p.org, nblk = p.nblk;
+  const bool causal = p.causal != 0;
+  const int npre = p.num_prefix;
+  const float c = p.c;
+  const int ngrp = (nblk + W - 1) / W;
+  int bh, grp;
+  decode_wg(ngrp, causal, bh, grp);
+  const int b = bh / p.H, hh = bh - b * p.H;
+  const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
+  const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
+  const T* V = reinterpret_cast<const T*>(p.v) + b * p.sv[0] + hh * p.sv[1];
+  T* O = reinterpret_cast<T*>(const_cast<void*>(p.o)) + b * p.so[0] + hh * p.so[1];
+
+  const int blk0 = nblk - (ngrp - grp) * W;
+  const int qblk = blk0 + wave;
+  const bool wave_on = qblk >= 0;
+  const int q0 = org + 32 * qblk;
+  const int qtok = q0 + n;
+  const bool qvalid = wave_on && qtok >= 0;
+  const int wg_qlast = org + 32 * (blk0 + W) - 1;
+  int hi = causal ? max(wg_qlast + 1, npre) : N;
+  hi = min(hi, N);
+  const int nkt_all = (nblk + KB - 1) / KB;
+  const int kshift = nkt_all * KB - nblk;
+  const int last_blk = (hi - 1 - org) >> 5;
+  const int nkt = (last_blk + kshift) / KB + 1;
+
+  frag qf[KS];
+#pragma unroll
+  for (int t = 0; t < KS; ++t)
+    qf[t] = (qvalid && 16 * t + 8 * h < D) ? ld8<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h) : zero_frag<T>();
+  float qoff = 0.f;
+  if constexpr (!SOFTMAX) {
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < KS; ++t) s += sumsq8<T>(qf[t]);
+    s += __shfl_xor(s, 32);
+    qoff = c * 0.5f * s;
+  }
+
+  f32x16_t oacc[ND];
+#pragma unroll
+  for (int d = 0; d < ND; ++d) oacc[d] = zero16();
+  float m_run = -__builtin_inff();
+  float l_run = 0.f;
+
+  Tile<T, BN, DP, NT> tk, tv;
+  {
+    const int tok0 = org + 32 * (-kshift);
+    tk.load(K, p.sk[2], tok0, N, D, tid);
+    tv.load(V, p.sv[2], tok0, N, D, tid);
+  }
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int buf = kt & 1;
+    tk.template store_rows<LDR>(sK[buf], tid);
+    tk.store_halfnorm(sKn[buf], tid);
+    tv.template store_trans<LDT>(sVt[buf], tid);
+    __syncthreads();
+    if (kt + 1 < nkt) {
+      const int tok1 = org + 32 * ((kt + 1) * KB - kshift);
+      tk.load(K, p.sk[2], tok1, N, D, tid);
+      tv.load(V, p.sv[2], tok1, N, D, tid);
+    }
+    if (wave_on) {
+      const int kblk0 = kt * KB - kshift;
+      f32x16_t s[KB];
+      bool act[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const int k0 = org + 32 * (kblk0 + kb);
+        act[kb] = (kblk0 + kb >= 0) && (!causal || k0 <= q0 + 31 || k0 < npre);
+        if (act[kb]) {
+          const bool full = k0 >= 0 && q0 >= 0 && (!causal || k0 + 31 <= q0 || k0 + 31 < npre);
+          const float* kn = sKn[buf] + 32 * kb + 4 * h;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(kn + 8 * g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s[kb][4 * g + e] = -v4[e];
+          }
+#pragma unroll
+          for (int t = 0; t < KS; ++t)
+            s[kb] = E::mma(ld8<T>(sK[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h), qf[t], s[kb]);
+          if (!full) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int j = k0 + crow(i, h);
+              const bool vis = j >= 0 && qtok >= 0 && (!causal || j <= qtok || j < npre);
+              if (!vis) s[kb][i] = -__builtin_inff();
+            }
+          }
+        }
+      }
+      float moff;
+      if constexpr (SOFTMAX) {
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+          if (act[kb]) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+          }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mt = mx * c;
+        if (__any(mt > m_run + kTau)) {
+          const float mnew = fmaxf(m_run, mt);
+          const float alpha = (mnew == -__builtin_inff()) ? 1.f : fast_exp2(m_run - mnew);
+          l_run *= alpha;
+#pragma unroll
+          for (int d = 0; d < ND; ++d) oacc[d] *= alpha;
+          m_run = mnew;
+        }
+        moff = (m_run == -__builtin_inff()) ? 0.f : m_run;
+      } else {
+        moff = qoff;
+      }
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        if (!act[kb]) continue;
+        frag pf[2];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float pv = fast_exp2(fmaf(s[kb][i], c, -moff));
+          if constexpr (SOFTMAX) l_run += pv;
+          pf[i >> 3][i & 7] = (T)pv;
+        }
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+            oacc[d] = E::mma(ld8<T>(sVt[buf] + (32 * d + n) * LDT + 32 * kb + 16 * t + 8 * h), pf[t], oacc[d]);
+      }
+    }
+  }
+
+  if (wave_on) {
+    float lsum = l_run;
+    if constexpr (SOFTMAX) lsum += __shfl_xor(lsum, 32);
+    const float inv = SOFTMAX ? 1.f / lsum : 1.f;
+    if (qvalid) {
+      T* orow = O + (int64_t)qtok * p.so[2];
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int dd = 32 * d + 8 * g + 4 * h;
+          if (dd < D) {
+            float v4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v4[e] = oacc[d][4 * g + e] * inv;
+            st4f<T>(orow + dd, v4);
+          }
+        }
+      if (SOFTMAX && h == 0) p.lse[(int64_t)bh * N + qtok] = m_run + __log2f(lsum);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, query-stationary: dQ.  Also produces, per query, Delta =
+// rowsum(O*dO) (softmax) or the norm offset c*0.5*||q||^2 written to the lse
+// workspace (non-softmax), both consumed by the dK/dV kernel launched next.
+// K (row-major and transposed), V (row-major) stream through LDS.
+// ---------------------------------------------------------------------------
+template <typename T, int DP, int W, int BN, bool SOFTMAX>
+__global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
+  typedef Elem<T> E;
+  typedef typename E::frag frag;
+  constexpr int NT = 64 * W, KB = BN / 32, KS = DP / 16, ND = DP / 32;
+  constexpr int LDR = DP + E::PAD, LDT = BN + E::PAD;
+  __shared__ __attribute__((aligned(16))) T sK[2][BN * LDR];
+  __shared__ __attribute__((aligned(16))) T sKt[2][DP * LDT];
+  __shared__ __attribute__((aligned(16))) T sV[2][BN * LDR];
+  __shared__ __attribute__((aligned(16))) float sKn[2][BN];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int N = p.N, D = p.D, org = p.org, nblk = p.nblk;
+  const bool causal = p.causal != 0;
+  const int npre = p.num_prefix;
+  const float c = p.c;
+  const int ngrp = (nblk + W - 1) / W;
+  int bh, grp;
+  decode_wg(ngrp, causal, bh, grp);
+  const int b = bh / p.H, hh = bh - b * p.H;
+  const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
+  const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
+  const T* V = reinterpret_cast<const T*>(p.v) + b * p.sv[0] + hh * p.sv[1];
+  const T* Og = reinterpret_cast<const T*>(p.o) + b * p.so[0] + hh * p.so[1];
+  const T* dO = reinterpret_cast<const T*>(p.dout) + b * p.sdo[0] + hh * p.sdo[1];
+  T* dQ = reinterpret_cast<T*>(p.dq) + b * p.sdq[0] + hh * p.sdq[1];
+
+  const int blk0 = nblk - (ngrp - grp) * W;
+  const int qblk = blk0 + wave;
+  const bool wave_on = qblk >= 0;
+  const int q0 = org + 32 * qblk;
+  const int qtok = q0 + n;
+  const bool qvalid = wave_on && qtok >= 0;
+  const int wg_qlast = org + 32 * (blk0 + W) - 1;
+  int hi = causal ? max(wg_qlast + 1, npre) : N;
+  hi = min(hi, N);
+  const int nkt_all = (nblk + KB - 1) / KB;
+  const int kshift = nkt_all * KB - nblk;
+  const int last_blk = (hi - 1 - org) >> 5;
+  const int nkt = (last_blk + kshift) / KB + 1;
+
+  frag qf[KS], df[KS];
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    const bool ok = qvalid && 16 * t + 8 * h < D;
+    qf[t] = ok ? ld8<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h) : zero_frag<T>();
+    df[t] = ok ? ld8<T>(dO + (int64_t)qtok * p.sdo[2] + 16 * t + 8 * h) : zero_frag<T>();
+  }
+  float off, dlt;
+  if constexpr (SOFTMAX) {
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      const bool ok = qvalid && 16 * t + 8 * h < D;
+      const frag of = ok ? ld8<T>(Og + (int64_t)qtok * p.so[2] + 16 * t + 8 * h) : zero_frag<T>();
+      s += dot8<T>(of, df[t]);
+    }
+    s += __shfl_xor(s, 32);
+    dlt = s;
+    off = qvalid ? p.lse[(int64_t)bh * N + qtok] : 0.f;
+    if (qvalid && h == 0) p.delta[(int64_t)bh * N + qtok] = dlt;
+  } else {
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < KS; ++t) s += sumsq8<T>(qf[t]);
+    s += __shfl_xor(s, 32);
+    off = c * 0.5f * s;
+    dlt = 0.f;
+    if (qvalid && h == 0) p.lse[(int64_t)bh * N + qtok] = off;
+  }
+
+  f32x16_t dqacc[ND];
+#pragma unroll
+  for (int d = 0; d < ND; ++d) dqacc[d] = zero16();
+  float rsum = 0.f;
+
+  Tile<T, BN, DP, NT> tk, tv;
+  {
+    const int tok0 = org + 32 * (-kshift);
+    tk.load(K, p.sk[2], tok0, N, D, tid);
+    tv.load(V, p.sv[2], tok0, N, D, tid);
+  }
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int buf = kt & 1;
+    tk.template store_rows<LDR>(sK[buf], tid);
+    tk.template store_trans<LDT>(sKt[buf], tid);
+    tk.store_halfnorm(sKn[buf], tid);
+    tv.template store_rows<LDR>(sV[buf], tid);
+    __syncthreads();
+    if (kt + 1 < nkt) {
+      const int tok1 = org + 32 * ((kt + 1) * KB - kshift);
+      tk.load(K, p.sk[2], tok1, N, D, tid);
+      tv.load(V, p.sv[2], tok1, N, D, tid);
+    }
+    if (wave_on) {
+      const int kblk0 = kt * KB - kshift;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const int k0 = org + 32 * (kblk0 + kb);
+        const bool act = (kblk0 + kb >= 0) && (!causal || k0 <= q0 + 31 || k0 < npre);
+        if (!act) continue;
+        const bool full = k0 >= 0 && q0 >= 0 && (!causal || k0 + 31 <= q0 || k0 + 31 < npre);
+        f32x16_t s, dp = zero16();
+        const float* kn = sKn[buf] + 32 * kb + 4 * h;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(kn + 8 * g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[4 * g + e] = -v4[e];
+        }
+#pragma unroll
+        for (int t = 0; t < KS; ++t) {
+          s = E::mma(ld8<T>(sK[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h), qf[t], s);
+          dp = E::mma(ld8<T>(sV[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h), df[t], dp);
+        }
+        if (!full) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int j = k0 + crow(i, h);
+            const bool vis = j >= 0 && qtok >= 0 && (!causal || j <= qtok || j < npre);
+            if (!vis) s[i] = -__builtin_inff();
+          }
+        }
+        frag sf[2];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float pv = fast_exp2(fmaf(s[i], c, -off));
+          const float ds = pv * (dp[i] - dlt);
+          if constexpr (!SOFTMAX) rsum += ds;
+          sf[i >> 3][i & 7] = (T)ds;
+        }
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+            dqacc[d] = E::mma(ld8<T>(sKt[buf] + (32 * d + n) * LDT + 32 * kb + 16 * t + 8 * h), sf[t], dqacc[d]);
+      }
+    }
+  }
+
+  if (wave_on) {
+    float rs = 0.f;
+    if constexpr (!SOFTMAX) rs = rsum + __shfl_xor(rsum, 32);
+    if (qvalid) {
+      const float g2 = 2.f * p.gamma;
+      T* drow = dQ + (int64_t)qtok * p.sdq[2];
+      const T* qrow = Q + (int64_t)qtok * p.sq[2];
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int dd = 32 * d + 8 * g + 4 * h;
+          if (dd < D) {
+            float v4[4];
+            if constexpr (SOFTMAX) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v4[e] = g2 * dqacc[d][4 * g + e];
+            } else {
+              float q4[4];
+              ld4f<T>(qrow + dd, q4);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v4[e] = g2 * (dqacc[d][4 * g + e] - rs * q4[e]);
+            }
+            st4f<T>(drow + dd, v4);
+          }
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, key-stationary: dK and dV.  One wave owns 32 keys (K and V held in
+// registers); BM-query tiles of Q and dO (row-major and transposed) plus the
+// per-query offset (L, or c*0.5*||q||^2) and Delta stream through LDS.
+// ---------------------------------------------------------------------------
+template <typename T, int DP, int W, int BM, bool SOFTMAX>
+__global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
+  typedef Elem<T> E;
+  typedef typename E::frag frag;
+  constexpr int NT = 64 * W, QB = BM / 32, KS = DP / 16, ND = DP / 32;
+  constexpr int LDR = DP + E::PAD, LDT = BM + E::PAD;
+  __shared__ __attribute__((aligned(16))) T sQ[2][BM * LDR];
+  __shared__ __attribute__((aligned(16))) T sQt[2][DP * LDT];
+  __shared__ __attribute__((aligned(16))) T sD[2][BM * LDR];
+  __shared__ __attribute__((aligned(16))) T sDt[2][DP * LDT];
+  __shared__ __attribute__((aligned(16))) float sOff[2][BM];
+  __shared__ __attribute__((aligned(16))) float sDel[2][BM];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int N = p.N, D = p.D, org = p.org, nblk = p.nblk;
+  const bool causal = p.causal != 0;
+  const int npre = p.num_prefix;
+  const float c = p.c;
+  const int ngrp = (nblk + W - 1) / W;
+  int bh, grp;
+  decode_wg(ngrp, false, bh, grp);
+  const int b = bh / p.H, hh = bh - b * p.H;
+  const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
+  const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
+  const T* V = reinterpret_cast<const T*>(p.v) + b * p.sv[0] + hh * p.sv[1];
+  const T* dO = reinterpret_cast<const T*>(p.dout) + b * p.sdo[0] + hh * p.sdo[1];
+  T* dK = reinterpret_cast<T*>(p.dk) + b * p.sdk[0] + hh * p.sdk[1];
+  T* dV = reinterpret_cast<T*>(p.dv) + b * p.sdv[0] + hh * p.sdv[1];
+  const float* offg = p.lse + (int64_t)bh * N;
+  const float* delg = SOFTMAX ? p.delta + (int64_t)bh * N : nullptr;
+
+  const int blk0 = nblk - (ngrp - grp) * W;
+  const int kblk = blk0 + wave;
+  const bool wave_on = kblk >= 0;
+  const int k0 = org + 32 * kblk;
+  const int ktok = k0 + n;
+  const bool kvalid = wave_on && ktok >= 0;
+
+  frag kf[KS], vf[KS];
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    const bool ok = kvalid && 16 * t + 8 * h < D;
+    kf[t] = ok ? ld8<T>(K + (int64_t)ktok * p.sk[2] + 16 * t + 8 * h) : zero_frag<T>();
+    vf[t] = ok ? ld8<T>(V + (int64_t)ktok * p.sv[2] + 16 * t + 8 * h) : zero_frag<T>();
+  }
+  float kn;
+  {
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < KS; ++t) s += sumsq8<T>(kf[t]);
+    s += __shfl_xor(s, 32);
+    kn = 0.5f * s;
+  }
+
+  f32x16_t dkacc[ND], dvacc[ND];
+#pragma unroll
+  for (int d = 0; d < ND; ++d) {
+    dkacc[d] = zero16();
+    dvacc[d] = zero16();
+  }
+  float csum = 0.f;
+
+  // Query range: causal keys are seen by queries at or after them, except
+  // prefix (register) keys, which every query sees.
+  const int wg_kfirst = max(org + 32 * max(blk0, 0), 0);
+  const int qlo = causal ? (wg_kfirst < npre ? 0 : wg_kfirst) : 0;
+  const int nqt_all = (nblk + QB - 1) / QB;
+  const int qshift = nqt_all * QB - nblk;
+  const int qt_lo = (((qlo - org) >> 5) + qshift) / QB;
+
+  Tile<T, BM, DP, NT> tq, td;
+  float offr = 0.f, delr = 0.f;
+  auto load_tile = [&](int qt) {
+    const int tok0 = org + 32 * (qt * QB - qshift);
+    tq.load(Q, p.sq[2], tok0, N, D, tid);
+    td.load(dO, p.sdo[2], tok0, N, D, tid);
+    if (tid < BM) {
+      const int tok = tok0 + tid;
+      const bool ok = tok >= 0 && tok < N;
+      offr = ok ? offg[tok] : 0.f;
+      if constexpr (SOFTMAX) delr = ok ? delg[tok] : 0.f;
+    }
+  };
+  load_tile(qt_lo);
+  for (int qt = qt_lo; qt < nqt_all; ++qt) {
+    const int buf = qt & 1;
+    tq.template store_rows<LDR>(sQ[buf], tid);
+    tq.template store_trans<LDT>(sQt[buf], tid);
+    td.template store_rows<LDR>(sD[buf], tid);
+    td.template store_trans<LDT>(sDt[buf], tid);
+    if (tid < BM) {
+      sOff[buf][tid] = offr;
+      sDel[buf][tid] = delr;
+    }
+    __syncthreads();
+    if (qt + 1 < nqt_all) load_tile(qt + 1);
+    if (wave_on) {
+      const int qblk0 = qt * QB - qshift;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const int q0 = org + 32 * (qblk0 + qb);
+        const bool act = (qblk0 + qb >= 0) && (!causal || q0 + 31 >= k0 || k0 < npre);
+        if (!act) continue;
+        const bool full = q0 >= 0 && k0 >= 0 && (!causal || q0 >= k0 + 31 || k0 + 31 < npre);
+        f32x16_t s, dp = zero16();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = -kn;
+#pragma unroll
+        for (int t = 0; t < KS; ++t) {
+          s = E::mma(ld8<T>(sQ[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h), kf[t], s);
+          dp = E::mma(ld8<T>(sD[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h), vf[t], dp);
+        }
+        if (!full) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int it = q0 + crow(i, h);
+            const bool vis = it >= 0 && ktok >= 0 && (!causal || ktok <= it || ktok < npre);
+            if (!vis) s[i] = -__builtin_inff();
+          }
+        }
+        float offv[16], delv[16];
+        {
+          const float* po = sOff[buf] + 32 * qb + 4 * h;
+          const float* pd = sDel[buf] + 32 * qb + 4 * h;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const f32x4_t o4 = *reinterpret_cast<const f32x4_t*>(po + 8 * g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) offv[4 * g + e] = o4[e];
+            if constexpr (SOFTMAX) {
+              const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(pd + 8 * g);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) delv[4 * g + e] = d4[e];
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) delv[4 * g + e] = 0.f;
+            }
+          }
+        }
+        frag pf[2], sf[2];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float pv = fast_exp2(fmaf(s[i], c, -offv[i]));
+          const float ds = pv * (dp[i] - delv[i]);
+          csum += ds;
+          pf[i >> 3][i & 7] = (T)pv;
+          sf[i >> 3][i & 7] = (T)ds;
+        }
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            dvacc[d] = E::mma(ld8<T>(sDt[buf] + (32 * d + n) * LDT + 32 * qb + 16 * t + 8 * h), pf[t], dvacc[d]);
+            dkacc[d] = E::mma(ld8<T>(sQt[buf] + (32 * d + n) * LDT + 32 * qb + 16 * t + 8 * h), sf[t], dkacc[d]);
+          }
+      }
+    }
+  }
+
+  if (wave_on) {
+    const float cs = csum + __shfl_xor(csum, 32);
+    if (kvalid) {
+      const float g2 = 2.f * p.gamma;
+      T* dkrow = dK + (int64_t)ktok * p.sdk[2];
+      T* dvrow = dV + (int64_t)ktok * p.sdv[2];
+      const T* krow = K + (int64_t)ktok * p.sk[2];
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int dd = 32 * d + 8 * g + 4 * h;
+          if (dd < D) {
+            float k4[4], a4[4], b4[4];
+            ld4f<T>(krow + dd, k4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              a4[e] = g2 * (dkacc[d][4 * g + e] - cs * k4[e]);
+              b4[e] = dvacc[d][4 * g + e];
+            }
+            st4f<T>(dkrow + dd, a4);
+            st4f<T>(dvrow + dd, b4);
+          }
+        }
+    }
+  }
+}
+
+}  // namespace rbf

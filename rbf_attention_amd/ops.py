@@ -1,0 +1,446 @@
+"""torch.library operators for RBF attention on MI355X.
+
+Drop-in surface of the reference (rbf_attention.py):
+  * ``rbf_attn_v5::scaled_fwd(q, k, v, is_causal) -> (out, L)``        (651-690)
+  * ``rbf_attn_v5::scaled_bwd(q, k, v, out, L, dout, is_causal, sm_scale)
+        -> (dq, dk, dv)``                                               (702-810)
+  * ``rbf_attn_v5::non_softmax_fwd(q, k, v, is_causal) -> out``        (1355-1391)
+  * ``rbf_attn_v5::non_softmax_bwd(q, k, v, dout, is_causal, sm_scale)
+        -> (dq, dk, dv)``                                               (1399-1480)
+  each with a fake (meta) implementation and autograd registration
+  (822-842, 1492-1511), plus ``run_triton_rbf`` / ``run_triton_non_softmax_rbf``
+  (848-853).
+
+Same names, schemas and semantics: gamma (the reference's ``sm_scale``) is
+1/sqrt(D) in the forward ops, L is the base-2 log-sum-exp of
+2*gamma*q.k - gamma*||k||^2, outputs are freshly allocated contiguous tensors,
+and the autograd backward ignores the gradient of L.
+
+Extensions, in a separate namespace so the reference schemas stay exact:
+``rbf_attn_amd::{scaled,non_softmax}_{fwd,bwd}_ex`` take an explicit
+``sm_scale`` (gamma) and ``num_prefix`` (keys j < num_prefix are visible to every
+query: register tokens).  ``run_triton_rbf(..., sm_scale=, num_prefix=)``
+routes to them when either differs from the reference default.
+
+Every op runs the HIP kernels of librbfattn.so; there is no CPU or PyTorch
+fallback.  Unsupported inputs raise.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+_V5 = "rbf_attn_v5"
+_EX = "rbf_attn_amd"
+
+
+# ---------------------------------------------------------------------------
+# Input handling
+# ---------------------------------------------------------------------------
+def _check_inputs(name: str, *ts: torch.Tensor) -> None:
+    q = ts[0]
+    if q.dim() != 4:
+        raise ValueError(f"{name}: expected (B, H, N, D) tensors, got q of shape {tuple(q.shape)}")
+    for t in ts:
+        if t.shape != q.shape:
+            raise ValueError(f"{name}: shape mismatch {tuple(t.shape)} vs {tuple(q.shape)}")
+        if t.dtype != q.dtype:
+            raise TypeError(f"{name}: dtype mismatch {t.dtype} vs {q.dtype}")
+        if t.device != q.device:
+            raise ValueError(f"{name}: device mismatch {t.device} vs {q.device}")
+    if q.dtype not in _lib.DTYPE_CODES:
+        raise TypeError(f"{name}: unsupported dtype {q.dtype} (bf16, fp16, fp32)")
+    if q.shape[-1] > 128:
+        raise ValueError(f"{name}: head dim {q.shape[-1]} > 128 is not supported")
+    if q.device.type != "cuda":
+        raise RuntimeError(
+            f"{name}: tensors are on {q.device}; the RBF attention kernels run only on a ROCm GPU "
+            "(there is no CPU fallback)"
+        )
+
+
+def _padded_dim(d: int) -> int:
+    return max(8, (d + 7) // 8 * 8)
+
+
+def _prep(t: torch.Tensor, dpad: int) -> torch.Tensor:
+    """Meet the C-ABI layout contract: unit last stride, 16-byte aligned base
+    and strides, head dim a multiple of 8.  Copies only when needed."""
+    d = t.shape[-1]
+    if dpad != d:
+        return torch.nn.functional.pad(t, (0, dpad - d))
+    esz = t.element_size()
+    ok = (
+        t.stride(-1) == 1
+        and t.data_ptr() % 16 == 0
+        and all((s * esz) % 16 == 0 for s in t.stride()[:3])
+    )
+    return t if ok else t.contiguous()
+
+
+def _base_args(variant: int, q: torch.Tensor, is_causal: bool, sm_scale: float, num_prefix: int, dpad: int):
+    B, H, N, _ = q.shape
+    a = _lib.Args()
+    a.abi_version = _lib.ABI_VERSION
+    a.variant = variant
+    a.dtype = _lib.DTYPE_CODES[q.dtype]
+    a.B, a.H, a.N, a.D = B, H, N, dpad
+    a.causal = 1 if is_causal else 0
+    a.num_prefix = int(num_prefix)
+    a.gamma = float(sm_scale)
+    return a
+
+
+def _launch(fn: str, a, device: torch.device) -> None:
+    with torch.cuda.device(device):
+        _lib.call(fn, a, torch.cuda.current_stream(device).cuda_stream)
+
+
+def _unpad(t: torch.Tensor, d: int) -> torch.Tensor:
+    return t if t.shape[-1] == d else t[..., :d].contiguous()
+
+
+# ---------------------------------------------------------------------------
+# Implementations (shared by the reference-schema ops and the _ex ops)
+# ---------------------------------------------------------------------------
+def _softmax_fwd(q, k, v, is_causal: bool, sm_scale: float, num_prefix: int):
+    _check_inputs("scaled_fwd", q, k, v)
+    B, H, N, D = q.shape
+    dp = _padded_dim(D)
+    q_, k_, v_ = _prep(q, dp), _prep(k, dp), _prep(v, dp)
+    out = torch.empty((B, H, N, dp), device=q.device, dtype=q.dtype)
+    L = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
+    a = _base_args(_lib.SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
+    a.q, a.k, a.v, a.o = (_lib.tensor_desc(t) for t in (q_, k_, v_, out))
+    a.lse = L.data_ptr()
+    _launch("rbf_attn_fwd", a, q.device)
+    return _unpad(out, D), L
+
+
+def _softmax_bwd(q, k, v, out, L, dout, is_causal: bool, sm_scale: float, num_prefix: int):
+    _check_inputs("scaled_bwd", q, k, v, out, dout)
+    B, H, N, D = q.shape
+    if L.shape != (B, H, N) or L.dtype != torch.float32:
+        raise ValueError(f"scaled_bwd: L must be float32 of shape {(B, H, N)}, got {L.dtype} {tuple(L.shape)}")
+    dp = _padded_dim(D)
+    q_, k_, v_, o_, do_ = (_prep(t, dp) for t in (q, k, v, out, dout))
+    L_ = L.contiguous()
+    delta = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
+    dq = torch.empty((B, H, N, dp), device=q.device, dtype=q.dtype)
+    dk = torch.empty_like(dq)
+    dv = torch.empty_like(dq)
+    a = _base_args(_lib.SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
+    a.q, a.k, a.v, a.o, a.dout = (_lib.tensor_desc(t) for t in (q_, k_, v_, o_, do_))
+    a.dq, a.dk, a.dv = (_lib.tensor_desc(t) for t in (dq, dk, dv))
+    a.lse = L_.data_ptr()
+    a.delta = delta.data_ptr()
+    _launch("rbf_attn_bwd", a, q.device)
+    return _unpad(dq, D), _unpad(dk, D), _unpad(dv, D)
+
+
+def _non_softmax_fwd(q, k, v, is_causal: bool, sm_scale: float, num_prefix: int):
+    _check_inputs("non_softmax_fwd", q, k, v)
+    B, H, N, D = q.shape
+    dp = _padded_dim(D)
+    q_, k_, v_ = _prep(q, dp), _prep(k, dp), _prep(v, dp)
+    out = torch.empty((B, H, N, dp), device=q.device, dtype=q.dtype)
+    a = _base_args(_lib.NON_SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
+    a.q, a.k, a.v, a.o = (_lib.tensor_desc(t) for t in (q_, k_, v_, out))
+    _launch("rbf_attn_fwd", a, q.device)
+    return _unpad(out, D)
+
+
+def _non_softmax_bwd(q, k, v, dout, is_causal: bool, sm_scale: float, num_prefix: int):
+    _check_inputs("non_softmax_bwd", q, k, v, dout)
+    B, H, N, D = q.shape
+    dp = _padded_dim(D)
+    q_, k_, v_, do_ = (_prep(t, dp) for t in (q, k, v, dout))
+    qoff = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
+    dq = torch.empty((B, H, N, dp), device=q.device, dtype=q.dtype)
+    dk = torch.empty_like(dq)
+    dv = torch.empty_like(dq)
+    a = _base_args(_lib.NON_SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
+    a.q, a.k, a.v, a.dout = (_lib.tensor_desc(t) for t in (q_, k_, v_, do_))
+    a.dq, a.dk, a.dv = (_lib.tensor_desc(t) for t in (dq, dk, dv))
+    a.lse = qoff.data_ptr()
+    _launch("rbf_attn_bwd", a, q.device)
+    return _unpad(dq, D), _unpad(dk, D), _unpad(dv, D)
+
+
+def _default_scale(q: torch.Tensor) -> float:
+    # rbf_attention.py:660, 827, 1362, 1496
+    return 1.0 / math.sqrt(q.shape[-1])
+
+
+# ---------------------------------------------------------------------------
+# Reference-schema ops: rbf_attn_v5::*
+# ---------------------------------------------------------------------------
+@torch.library.custom_op(f"{_V5}::scaled_fwd", mutates_args=())
+def rbf_scaled_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, is_causal: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    return _softmax_fwd(q, k, v, is_causal, _default_scale(q), 0)
+
+
+@rbf_scaled_fwd.register_fake
+def _(q, k, v, is_causal):
+    B, H, N, _ = q.shape
+    return (
+        torch.empty_like(q, memory_format=torch.contiguous_format),
+        torch.empty((B, H, N), device=q.device, dtype=torch.float32),
+    )
+
+
+@torch.library.custom_op(f"{_V5}::scaled_bwd", mutates_args=())
+def rbf_scaled_bwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    out: torch.Tensor,
+    L: torch.Tensor,
+    dout: torch.Tensor,
+    is_causal: bool,
+    sm_scale: float,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return _softmax_bwd(q, k, v, out, L, dout, is_causal, sm_scale, 0)
+
+
+@rbf_scaled_bwd.register_fake
+def _(q, k, v, out, L, dout, is_causal, sm_scale):
+    return (
+        torch.empty_like(q, memory_format=torch.contiguous_format),
+        torch.empty_like(k, memory_format=torch.contiguous_format),
+        torch.empty_like(v, memory_format=torch.contiguous_format),
+    )
+
+
+def _scaled_setup_context(ctx, inputs, output):
+    q, k, v, is_causal = inputs
+    out, L = output
+    ctx.save_for_backward(q, k, v, out, L)
+    ctx.is_causal = is_causal
+    ctx.sm_scale = _default_scale(q)
+
+
+def _scaled_backward(ctx, dout, dL):
+    # dL is ignored, as in the reference (rbf_attention.py:830-835).
+    q, k, v, out, L = ctx.saved_tensors
+    dq, dk, dv = torch.ops.rbf_attn_v5.scaled_bwd(q, k, v, out, L, dout, ctx.is_causal, ctx.sm_scale)
+    return dq, dk, dv, None
+
+
+torch.library.register_autograd(f"{_V5}::scaled_fwd", _scaled_backward, setup_context=_scaled_setup_context)
+
+
+@torch.library.custom_op(f"{_V5}::non_softmax_fwd", mutates_args=())
+def rbf_non_softmax_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, is_causal: bool) -> torch.Tensor:
+    return _non_softmax_fwd(q, k, v, is_causal, _default_scale(q), 0)
+
+
+@rbf_non_softmax_fwd.register_fake
+def _(q, k, v, is_causal):
+    return torch.empty_like(q, memory_format=torch.contiguous_format)
+
+
+@torch.library.custom_op(f"{_V5}::non_softmax_bwd", mutates_args=())
+def rbf_non_softmax_bwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    dout: torch.Tensor,
+    is_causal: bool,
+    sm_scale: float,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return _non_softmax_bwd(q, k, v, dout, is_causal, sm_scale, 0)
+
+
+@rbf_non_softmax_bwd.register_fake
+def _(q, k, v, dout, is_causal, sm_scale):
+    return (
+        torch.empty_like(q, memory_format=torch.contiguous_format),
+        torch.empty_like(k, memory_format=torch.contiguous_format),
+        torch.empty_like(v, memory_format=torch.contiguous_format),
+    )
+
+
+def _non_softmax_setup_context(ctx, inputs, output):
+    q, k, v, is_causal = inputs
+    ctx.save_for_backward(q, k, v)
+    ctx.is_causal = is_causal
+    ctx.sm_scale = _default_scale(q)
+
+
+def _non_softmax_backward(ctx, dout):
+    q, k, v = ctx.saved_tensors
+    dq, dk, dv = torch.ops.rbf_attn_v5.non_softmax_bwd(q, k, v, dout, ctx.is_causal, ctx.sm_scale)
+    return dq, dk, dv, None
+
+
+torch.library.register_autograd(
+    f"{_V5}::non_softmax_fwd", _non_softmax_backward, setup_context=_non_softmax_setup_context
+)
+
+
+# ---------------------------------------------------------------------------
+# Extended ops: explicit gamma (sm_scale) and register-prefix visibility.
+# ---------------------------------------------------------------------------
+@torch.library.custom_op(f"{_EX}::scaled_fwd_ex", mutates_args=())
+def rbf_scaled_fwd_ex(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, is_causal: bool, sm_scale: float, num_prefix: int
+) -> tuple[torch.Tensor, torch.Tensor]:
+    return _softmax_fwd(q, k, v, is_causal, sm_scale, num_prefix)
+
+
+@rbf_scaled_fwd_ex.register_fake
+def _(q, k, v, is_causal, sm_scale, num_prefix):
+    B, H, N, _ = q.shape
+    return (
+        torch.empty_like(q, memory_format=torch.contiguous_format),
+        torch.empty((B, H, N), device=q.device, dtype=torch.float32),
+    )
+
+
+@torch.library.custom_op(f"{_EX}::scaled_bwd_ex", mutates_args=())
+def rbf_scaled_bwd_ex(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    out: torch.Tensor,
+    L: torch.Tensor,
+    dout: torch.Tensor,
+    is_causal: bool,
+    sm_scale: float,
+    num_prefix: int,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return _softmax_bwd(q, k, v, out, L, dout, is_causal, sm_scale, num_prefix)
+
+
+@rbf_scaled_bwd_ex.register_fake
+def _(q, k, v, out, L, dout, is_causal, sm_scale, num_prefix):
+    return tuple(torch.empty_like(t, memory_format=torch.contiguous_format) for t in (q, k, v))
+
+
+def _scaled_ex_setup_context(ctx, inputs, output):
+    q, k, v, is_causal, sm_scale, num_prefix = inputs
+    out, L = output
+    ctx.save_for_backward(q, k, v, out, L)
+    ctx.is_causal, ctx.sm_scale, ctx.num_prefix = is_causal, sm_scale, num_prefix
+
+
+def _scaled_ex_backward(ctx, dout, dL):
+    q, k, v, out, L = ctx.saved_tensors
+    dq, dk, dv = torch.ops.rbf_attn_amd.scaled_bwd_ex(
+        q, k, v, out, L, dout, ctx.is_causal, ctx.sm_scale, ctx.num_prefix
+    )
+    return dq, dk, dv, None, None, None
+
+
+torch.library.register_autograd(f"{_EX}::scaled_fwd_ex", _scaled_ex_backward, setup_context=_scaled_ex_setup_context)
+
+
+@torch.library.custom_op(f"{_EX}::non_softmax_fwd_ex", mutates_args=())
+def rbf_non_softmax_fwd_ex(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, is_causal: bool, sm_scale: float, num_prefix: int
+) -> torch.Tensor:
+    return _non_softmax_fwd(q, k, v, is_causal, sm_scale, num_prefix)
+
+
+@rbf_non_softmax_fwd_ex.register_fake
+def _(q, k, v, is_causal, sm_scale, num_prefix):
+    return torch.empty_like(q, memory_format=torch.contiguous_format)
+
+
+@torch.library.custom_op(f"{_EX}::non_softmax_bwd_ex", mutates_args=())
+def rbf_non_softmax_bwd_ex(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    dout: torch.Tensor,
+    is_causal: bool,
+    sm_scale: float,
+    num_prefix: int,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return _non_softmax_bwd(q, k, v, dout, is_causal, sm_scale, num_prefix)
+
+
+@rbf_non_softmax_bwd_ex.register_fake
+def _(q, k, v, dout, is_causal, sm_scale, num_prefix):
+    return tuple(torch.empty_like(t, memory_format=torch.contiguous_format) for t in (q, k, v))
+
+
+def _non_softmax_ex_setup_context(ctx, inputs, output):
+    q, k, v, is_causal, sm_scale, num_prefix = inputs
+    ctx.save_for_backward(q, k, v)
+    ctx.is_causal, ctx.sm_scale, ctx.num_prefix = is_causal, sm_scale, num_prefix
+
+
+def _non_softmax_ex_backward(ctx, dout):
+    q, k, v = ctx.saved_tensors
+    dq, dk, dv = torch.ops.rbf_attn_amd.non_softmax_bwd_ex(
+        q, k, v, dout, ctx.is_causal, ctx.sm_scale, ctx.num_prefix
+    )
+    return dq, dk, dv, None, None, None
+
+
+torch.library.register_autograd(
+    f"{_EX}::non_softmax_fwd_ex", _non_softmax_ex_backward, setup_context=_non_softmax_ex_setup_context
+)
+
+
+# ---------------------------------------------------------------------------
+# Public wrappers (rbf_attention.py:848-853) and autograd.Function aliases.
+# ---------------------------------------------------------------------------
+def run_triton_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0):
+    """Softmax RBF attention.  With the default ``sm_scale`` (1/sqrt(D)) and
+    ``num_prefix=0`` this is exactly the reference's ``run_triton_rbf``."""
+    if sm_scale is None and num_prefix == 0:
+        return torch.ops.rbf_attn_v5.scaled_fwd(q, k, v, is_causal)[0]
+    scale = _default_scale(q) if sm_scale is None else float(sm_scale)
+    return torch.ops.rbf_attn_amd.scaled_fwd_ex(q, k, v, is_causal, scale, int(num_prefix))[0]
+
+
+def run_triton_non_softmax_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0):
+    """Non-softmax RBF attention, sum_j exp(-gamma||q_i-k_j||^2) v_j."""
+    if sm_scale is None and num_prefix == 0:
+        return torch.ops.rbf_attn_v5.non_softmax_fwd(q, k, v, is_causal)
+    scale = _default_scale(q) if sm_scale is None else float(sm_scale)
+    return torch.ops.rbf_attn_amd.non_softmax_fwd_ex(q, k, v, is_causal, scale, int(num_prefix))
+
+
+class TritonRBFAttention(torch.autograd.Function):
+    """``TritonRBFAttention.apply(q, k, v, is_causal=True, sm_scale=None,
+    num_prefix=0)`` -> out.  Same kernels as ``run_triton_rbf``."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, is_causal=True, sm_scale=None, num_prefix=0):
+        scale = _default_scale(q) if sm_scale is None else float(sm_scale)
+        out, L = _softmax_fwd(q, k, v, bool(is_causal), scale, int(num_prefix))
+        ctx.save_for_backward(q, k, v, out, L)
+        ctx.cfg = (bool(is_causal), scale, int(num_prefix))
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, L = ctx.saved_tensors
+        dq, dk, dv = _softmax_bwd(q, k, v, out, L, dout, *ctx.cfg)
+        return dq, dk, dv, None, None, None
+
+
+class TritonNonSoftmaxRBFAttention(torch.autograd.Function):
+    """``TritonNonSoftmaxRBFAttention.apply(q, k, v, is_causal=True,
+    sm_scale=None, num_prefix=0)`` -> out."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, is_causal=True, sm_scale=None, num_prefix=0):
+        scale = _default_scale(q) if sm_scale is None else float(sm_scale)
+        out = _non_softmax_fwd(q, k, v, bool(is_causal), scale, int(num_prefix))
+        ctx.save_for_backward(q, k, v)
+        ctx.cfg = (bool(is_causal), scale, int(num_prefix))
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v = ctx.saved_tensors
+        dq, dk, dv = _non_softmax_bwd(q, k, v, dout, *ctx.cfg)
+        return dq, dk, dv, None, None, None

@@ -1,0 +1,130 @@
+"""CPU tests of the C-ABI library: it loads, exports every symbol that
+include/rbf_attn.h declares, and rejects bad arguments with the documented
+error codes before any HIP call (no GPU work is issued here)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch  # noqa: F401  (binds the library to torch's HIP runtime)
+
+from rbf_attention_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "rbf_attn.h")
+
+
+def header_functions():
+    src = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(rbf_attn_\w+)\s*\(", src, re.M)))
+
+
+def header_define(name):
+    m = re.search(rf"#define\s+{name}\s+(-?\d+)", open(HEADER).read())
+    return int(m.group(1))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} missing: run `python -m rbf_attention_amd.build` (or __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_exports_match_header(lib):
+    names = header_functions()
+    assert set(names) == set(_lib.EXPORTS), names
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_abi_version(lib):
+    assert lib.rbf_attn_abi_version() == header_define("RBF_ATTN_ABI_VERSION") == _lib.ABI_VERSION
+
+
+def test_error_codes_match_header():
+    for code, name in _lib.ERRORS.items():
+        assert header_define(f"RBF_ATTN_{name}") == code
+
+
+def test_struct_layout():
+    # 10 int32/float fields, 8 tensors of 32 bytes, 2 pointers
+    assert ctypes.sizeof(_lib.Tensor) == 32
+    assert _lib.Args.q.offset == 40
+    assert ctypes.sizeof(_lib.Args) == 40 + 8 * 32 + 16
+
+
+FAKE = 0x10000  # aligned, never dereferenced: every call below fails validation or is empty
+
+
+def good_args(**over):
+    a = _lib.Args()
+    a.abi_version = 1
+    a.variant = 0
+    a.dtype = 0
+    a.B, a.H, a.N, a.D = 2, 3, 64, 64
+    a.causal = 1
+    a.num_prefix = 0
+    a.gamma = 0.125
+    for i, f in enumerate(("q", "k", "v", "o", "dout", "dq", "dk", "dv")):
+        setattr(a, f, _lib.Tensor(FAKE + 0x100000 * i, 3 * 64 * 64, 64 * 64, 64))
+    a.lse = FAKE + 0x1000000
+    a.delta = FAKE + 0x2000000
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+def call(lib, fn, a):
+    return getattr(lib, fn)(ctypes.byref(a) if a is not None else None, None)
+
+
+@pytest.mark.parametrize("fn", ["rbf_attn_fwd", "rbf_attn_bwd"])
+@pytest.mark.parametrize(
+    "over,code",
+    [
+        (dict(abi_version=2), -1),
+        (dict(variant=5), -1),
+        (dict(dtype=7), -2),
+        (dict(D=60), -4),
+        (dict(D=136), -4),
+        (dict(D=0), -4),
+        (dict(B=-1), -5),
+        (dict(causal=2), -1),
+        (dict(num_prefix=-1), -1),
+        (dict(gamma=0.0), -1),
+        (dict(gamma=float("nan")), -1),
+        (dict(q=_lib.Tensor(None, 0, 0, 0)), -6),
+        (dict(k=_lib.Tensor(FAKE + 2, 3 * 64 * 64, 64 * 64, 64)), -3),
+        (dict(v=_lib.Tensor(FAKE, 3 * 64 * 64, 64 * 64, 63)), -3),
+        (dict(lse=None), -6),
+    ],
+)
+def test_validation(lib, fn, over, code):
+    a = good_args(**over)
+    assert call(lib, fn, a) == code
+    assert lib.rbf_attn_last_error().decode()
+
+
+def test_null_args(lib):
+    assert call(lib, "rbf_attn_fwd", None) == -1
+    assert call(lib, "rbf_attn_bwd", None) == -1
+
+
+def test_bwd_requires_delta_for_softmax_only(lib):
+    assert call(lib, "rbf_attn_bwd", good_args(delta=None, N=0)) == -6
+    assert call(lib, "rbf_attn_bwd", good_args(delta=None, N=0, variant=1)) == 0
+
+
+def test_fp32_alignment(lib):
+    # fp32 row stride of 4 elements = 16 bytes is fine; 2 elements is not
+    a = good_args(dtype=2, N=0)
+    assert call(lib, "rbf_attn_fwd", a) == 0
+    a = good_args(dtype=2, N=0, q=_lib.Tensor(FAKE, 64, 64, 2))
+    assert call(lib, "rbf_attn_fwd", a) == -3
+
+
+def test_empty_problem_is_noop(lib):
+    for over in (dict(B=0), dict(H=0), dict(N=0)):
+        assert call(lib, "rbf_attn_fwd", good_args(**over)) == 0
+        assert call(lib, "rbf_attn_bwd", good_args(**over)) == 0
+        assert lib.rbf_attn_last_error().decode() == ""

@@ -1,0 +1,229 @@
+"""GPU parity of the HIP kernels against the CPU oracle (float64 restatement
+of the reference math, oracle/rbf_oracle.py) on identical seeded inputs.
+
+Tolerances (from the build's target):
+  * fp32 inputs: max-abs error <= 1e-4 on O, dQ, dK, dV.
+  * bf16 / fp16 inputs: relative L2 error <= 1e-2, and elementwise
+    |got - ref| <= 2e-2 + 2^-8 |ref|.  The 2^-8 |ref| term is the half-ulp
+    of a bf16 result: storing an output of magnitude >= 8 in bf16 alone
+    moves it by up to 2^-8 of its value, more than 2e-2.
+Big configurations are compared on sampled (b, h) slices -- every slice is an
+independent problem -- plus size-independent properties at full size.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import rbf_attention_amd as ra
+from oracle import rbf_oracle as ro
+from rbf_attention_amd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+HALF_ULP_BF16 = 2.0 ** -8
+
+
+def np64(t):
+    return t.detach().to("cpu", torch.float64).numpy()
+
+
+def check(name, got, ref, dtype):
+    got = np64(got)
+    err = np.abs(got - ref)
+    rel_l2 = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+    info = f"{name}: max_abs={err.max():.3e} rel_l2={rel_l2:.3e} max|ref|={np.abs(ref).max():.3e}"
+    print(info, flush=True)
+    assert np.isfinite(got).all(), f"{name}: non-finite values"
+    if dtype == torch.float32:
+        assert err.max() <= 1e-4, info
+    else:
+        assert rel_l2 <= 1e-2, info
+        bad = err > 2e-2 + HALF_ULP_BF16 * np.abs(ref)
+        assert not bad.any(), info + f" ({bad.sum()} elements out of bound)"
+
+
+def run_ours(q, k, v, do, softmax, causal, gamma, num_prefix):
+    q, k, v = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    fn = ra.run_triton_rbf if softmax else ra.run_triton_non_softmax_rbf
+    out = fn(q, k, v, causal, sm_scale=gamma, num_prefix=num_prefix)
+    out.backward(do)
+    torch.cuda.synchronize()
+    return out, q.grad, k.grad, v.grad
+
+
+def oracle_all(q, k, v, do, softmax, causal, gamma, num_prefix, sl=None):
+    arrs = [np64(t) for t in (q, k, v, do)]
+    if sl is not None:
+        arrs = [a[sl] for a in arrs]
+    qn, kn, vn, don = arrs
+    if softmax:
+        O, L = ro.softmax_forward(qn, kn, vn, gamma, causal, num_prefix)
+        g = ro.softmax_backward(qn, kn, vn, don, gamma, causal, num_prefix)
+        return (O,) + g, L
+    O = ro.non_softmax_forward(qn, kn, vn, gamma, causal, num_prefix)
+    return (O,) + ro.non_softmax_backward(qn, kn, vn, don, gamma, causal, num_prefix), None
+
+
+def compare_case(q, k, v, do, softmax=True, causal=True, gamma=None, num_prefix=0, sl=None, tag=""):
+    D = q.shape[-1]
+    g = gamma if gamma is not None else 1.0 / math.sqrt(D)
+    print(f"case {tag} shape={tuple(q.shape)} {q.dtype} softmax={softmax} causal={causal} "
+          f"gamma={g:.5f} num_prefix={num_prefix}", flush=True)
+    outs = run_ours(q, k, v, do, softmax, causal, gamma, num_prefix)
+    refs, _ = oracle_all(q, k, v, do, softmax, causal, g, num_prefix, sl)
+    for name, got, ref in zip(("O", "dQ", "dK", "dV"), outs, refs):
+        check(f"{tag} {name}", got if sl is None else got[sl], ref, q.dtype)
+    return outs
+
+
+def to_dev(ts, dev):
+    return [t.to(dev) for t in ts]
+
+
+# ---------------------------------------------------------------------------
+# BASELINE configurations
+# ---------------------------------------------------------------------------
+def test_c1_tiny_fp32(cuda_device):
+    w = wl.C1_TINY
+    q, k, v, do = to_dev(wl.make_inputs(w), cuda_device)
+    compare_case(q, k, v, do, gamma=w.sm_scale, tag="C1")
+
+
+def test_c1_reference_default_gamma_through_v5_ops(cuda_device):
+    """gamma = 1/sqrt(D) through torch.ops.rbf_attn_v5 and its autograd."""
+    w = wl.C1_TINY
+    q, k, v, do = to_dev(wl.make_inputs(w), cuda_device)
+    compare_case(q, k, v, do, gamma=None, tag="C1-v5")
+
+
+def test_c1_lse_matches_oracle(cuda_device):
+    w = wl.C1_TINY
+    q, k, v, _ = to_dev(wl.make_inputs(w), cuda_device)
+    out, L = torch.ops.rbf_attn_amd.scaled_fwd_ex(q, k, v, True, w.sm_scale, 0)
+    _, Lref = ro.softmax_forward(np64(q), np64(k), np64(v), w.sm_scale)
+    err = np.abs(np64(L) - Lref).max()
+    print(f"L max_abs={err:.3e}")
+    assert err <= 1e-4
+
+
+@pytest.mark.parametrize("gamma_kind", ["baseline", "reference"])
+def test_c2_model_bf16(cuda_device, gamma_kind):
+    w = wl.C2_MODEL
+    q, k, v, do = to_dev(wl.make_inputs(w), cuda_device)
+    gamma = w.sm_scale if gamma_kind == "baseline" else None
+    compare_case(q, k, v, do, gamma=gamma, tag=f"C2-{gamma_kind}")
+
+
+def test_c2_registers_visible_to_all(cuda_device):
+    w = wl.C2_MODEL.with_(B=4)
+    q, k, v, do = to_dev(wl.make_inputs(w), cuda_device)
+    compare_case(q, k, v, do, gamma=w.sm_scale, num_prefix=4, tag="C2-prefix4")
+
+
+def test_c3_long_bf16_sampled(cuda_device):
+    w = wl.C3_LONG
+    q, k, v, do = to_dev(wl.make_inputs(w), cuda_device)
+    sl = (slice(1, 2), slice(5, 6))  # one (b, h) slice checked against the oracle
+    outs = compare_case(q, k, v, do, gamma=w.sm_scale, sl=sl, tag="C3")
+    # full-size properties: finite everywhere; the zero register row 0 sees only
+    # key 0 (v_0 = 0), so O[:, :, 0] == 0 exactly.
+    for t in outs:
+        assert torch.isfinite(t).all()
+    assert (outs[0][:, :, 0] == 0).all()
+
+
+def test_c4_nonsoftmax_bf16_sampled(cuda_device):
+    w = wl.C4_NONSOFTMAX
+    q, k, v, do = to_dev(wl.make_inputs(w), cuda_device)
+    sl = (slice(0, 16, 5), slice(0, 8, 3))  # 4 x 3 slices
+    outs = compare_case(q, k, v, do, softmax=False, gamma=w.sm_scale, sl=sl, tag="C4")
+    for t in outs:
+        assert torch.isfinite(t).all()
+
+
+# ---------------------------------------------------------------------------
+# Shapes, dtypes, masks, variants
+# ---------------------------------------------------------------------------
+def rand_inputs(B, H, N, D, dtype, dev, std=1.0, seed=0, key_scale=0.0):
+    w = wl.Workload("adhoc", B=B, H=H, content=N, D=D, dtype={torch.bfloat16: "bf16", torch.float16: "fp16",
+                                                            torch.float32: "fp32"}[dtype],
+                    registers=0, std=std, key_lognormal=key_scale, seed=seed)
+    return to_dev(wl.make_inputs(w), dev)
+
+
+@pytest.mark.parametrize("N", [1, 2, 31, 32, 33, 64, 65, 100, 129, 255])
+@pytest.mark.parametrize("softmax", [True, False])
+def test_ragged_lengths(cuda_device, N, softmax):
+    q, k, v, do = rand_inputs(2, 2, N, 64, torch.bfloat16, cuda_device, std=1.0 if softmax else 0.5, seed=N)
+    compare_case(q, k, v, do, softmax=softmax, tag=f"N{N}")
+
+
+@pytest.mark.parametrize("D", [8, 16, 40, 60, 72, 96, 128])
+def test_head_dims(cuda_device, D):
+    q, k, v, do = rand_inputs(1, 3, 77, D, torch.bfloat16, cuda_device, seed=D)
+    compare_case(q, k, v, do, tag=f"D{D}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("softmax", [True, False])
+def test_dtypes(cuda_device, dtype, softmax):
+    q, k, v, do = rand_inputs(2, 2, 150, 64, dtype, cuda_device, std=1.0 if softmax else 0.5, seed=3)
+    compare_case(q, k, v, do, softmax=softmax, tag=f"{dtype}")
+
+
+@pytest.mark.parametrize("causal,num_prefix", [(False, 0), (True, 4), (True, 40), (True, 300)])
+@pytest.mark.parametrize("softmax", [True, False])
+def test_masks(cuda_device, causal, num_prefix, softmax):
+    q, k, v, do = rand_inputs(1, 2, 200, 64, torch.bfloat16, cuda_device, std=1.0 if softmax else 0.5, seed=7)
+    compare_case(q, k, v, do, softmax=softmax, causal=causal, num_prefix=num_prefix, gamma=0.0625,
+                 tag=f"mask c{causal} p{num_prefix}")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_heavy_tailed_keys(cuda_device, D):
+    q, k, v, do = rand_inputs(2, 4, 300, D, torch.bfloat16, cuda_device, seed=11, key_scale=0.5)
+    compare_case(q, k, v, do, gamma=1.0 / (2 * math.sqrt(D)), tag=f"lognormal D{D}")
+
+
+def test_strided_views_like_the_model(cuda_device):
+    """q/k/v as views of one packed projection, dout as a permuted view
+    (rbf_attention.py:1659-1662, 1761)."""
+    B, N, H, D = 2, 130, 4, 64
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn(B, N, 3 * H * D, generator=g).to(torch.bfloat16).to(cuda_device)
+    q, k, v = qkv.view(B, N, 3, H, D).permute(2, 0, 3, 1, 4)
+    do = torch.randn(B, N, H, D, generator=g).to(torch.bfloat16).to(cuda_device).permute(0, 2, 1, 3)
+    assert not q.is_contiguous() and not do.is_contiguous()
+    compare_case(q, k, v, do, tag="strided")
+
+
+def test_deterministic(cuda_device):
+    q, k, v, do = rand_inputs(2, 4, 300, 64, torch.bfloat16, cuda_device, seed=21)
+    a = run_ours(q, k, v, do, True, True, None, 0)
+    b = run_ours(q, k, v, do, True, True, None, 0)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_autograd_function_aliases(cuda_device):
+    q, k, v, do = rand_inputs(1, 2, 96, 64, torch.bfloat16, cuda_device, seed=4)
+    ref = run_ours(q, k, v, do, True, True, None, 0)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = ra.TritonRBFAttention.apply(qq, kk, vv, True)
+    out.backward(do)
+    for x, y in zip((out, qq.grad, kk.grad, vv.grad), ref):
+        assert torch.equal(x, y)
+    ref2 = run_ours(q, k, v, do * 0.5, False, True, None, 0)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = ra.TritonNonSoftmaxRBFAttention.apply(qq, kk, vv, True)
+    out.backward(do * 0.5)
+    for x, y in zip((out, qq.grad, kk.grad, vv.grad), ref2):
+        assert torch.equal(x, y)
+
+
+def test_empty_batch(cuda_device):
+    q = torch.zeros(0, 2, 16, 64, device=cuda_device, dtype=torch.bfloat16)
+    out = ra.run_triton_rbf(q, q, q)
+    assert out.shape == q.shape
