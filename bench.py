@@ -88,6 +88,8 @@ def main() -> int:
     ap.add_argument("--workload", default="c2_model_bf16")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="run one device copy of this many MiB before timing (calibrates HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -129,6 +131,13 @@ def main() -> int:
         fwd()
         bwd()
 
+    if args.copy_probe_mb:
+        src = torch.empty(args.copy_probe_mb << 18, device=dev, dtype=torch.float32).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     log(f"workload {w.name}: B={w.B} H={w.H} N={w.N} D={w.D} {w.dtype} causal={w.causal} gamma={w.sm_scale:.6f}")
     for _ in range(args.warmup):
         step()

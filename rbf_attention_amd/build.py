@@ -23,13 +23,16 @@ LIB_NAME = "librbfattn.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = os.environ.get("RBF_ATTN_ARCH", "gfx950")
 
-# Packed-FP32 VALU ops are disabled for all device code.
+# Packed-FP32 VALU ops are disabled for all device code.  MFMA accumulators
+# are kept in ordinary VGPRs (the VGPR form of the MFMA instructions), so the
+# softmax VALU work reads them without AGPR<->VGPR copies.
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
     "-Wno-unused-command-line-argument",

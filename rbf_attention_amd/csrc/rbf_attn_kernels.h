@@ -158,6 +158,14 @@ __device__ inline int swap23(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 
 // Row of accumulator element i held by lane half h (32x32 MFMA C layout).
 __device__ inline int crow(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
 
+// Offset of the 8-token chunk starting at tile-local token position p8
+// (a multiple of 8) in feature row `feat` of a transposed tile with ROWS
+// tokens (see Tile::store_trans).
+template <int ROWS>
+__device__ inline int tchunk(int feat, int p8) {
+  return (((p8 >> 3) ^ ((feat >> 3) & (ROWS / 8 - 1))) << 3);
+}
+
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ inline f32x16_t zero16() {
@@ -233,7 +241,10 @@ struct Tile {
     }
   }
 
-  // lds[feature * LDT + swap23(row)]
+  // lds[feature * LDT + tpos(feature, row)]: the token axis is stored in
+  // swap23 order and its 8-element chunks are XOR-swizzled by feature/8, so
+  // that the 8 feature rows one store instruction touches fall in different
+  // LDS banks while an 8-token chunk stays contiguous for the MFMA reads.
   template <int LDT>
   __device__ inline void store_trans(T* lds, int tid) const {
 #pragma unroll
@@ -242,17 +253,19 @@ struct Tile {
       if (UNITS % NT != 0 && u >= UNITS) continue;
       const int rp = u / CPR, dc = u % CPR;
       const int pos = swap23(2 * rp);  // even; row 2rp+1 lands at pos+1
+      // every feature row 8dc + c shares the swizzle value dc
+      const int spos = (((pos >> 3) ^ (dc & (ROWS / 8 - 1))) << 3) | (pos & 7);
       if constexpr (sizeof(T) == 2) {
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
           const uint32_t w = bits16<T>(r[j][0][c]) | (bits16<T>(r[j][1][c]) << 16);
-          *reinterpret_cast<uint32_t*>(lds + (dc * 8 + c) * LDT + pos) = w;
+          *reinterpret_cast<uint32_t*>(lds + (dc * 8 + c) * LDT + spos) = w;
         }
       } else {
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-          lds[(dc * 8 + c) * LDT + pos] = r[j][0][c];
-          lds[(dc * 8 + c) * LDT + pos + 1] = r[j][1][c];
+          lds[(dc * 8 + c) * LDT + spos] = r[j][0][c];
+          lds[(dc * 8 + c) * LDT + spos + 1] = r[j][1][c];
         }
       }
     }
@@ -304,7 +317,8 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) T sVt[2][DP * LDT];
   __shared__ __attribute__((aligned(16))) float sKn[2][BN];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably wave-uniform
   const int N = p.N, D = p.D, org = p.org, nblk = p.nblk;
   const bool causal = p.causal != 0;
   const int npre = p.num_prefix;
@@ -435,7 +449,8 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
         for (int d = 0; d < ND; ++d)
 #pragma unroll
           for (int t = 0; t < 2; ++t)
-            oacc[d] = E::mma(ld8<T>(sVt[buf] + (32 * d + n) * LDT + 32 * kb + 16 * t + 8 * h), pf[t], oacc[d]);
+            oacc[d] = E::mma(ld8<T>(sVt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h)),
+                             pf[t], oacc[d]);
       }
     }
   }
@@ -480,7 +495,8 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) T sV[2][BN * LDR];
   __shared__ __attribute__((aligned(16))) float sKn[2][BN];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably wave-uniform
   const int N = p.N, D = p.D, org = p.org, nblk = p.nblk;
   const bool causal = p.causal != 0;
   const int npre = p.num_prefix;
@@ -604,7 +620,8 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
         for (int d = 0; d < ND; ++d)
 #pragma unroll
           for (int t = 0; t < 2; ++t)
-            dqacc[d] = E::mma(ld8<T>(sKt[buf] + (32 * d + n) * LDT + 32 * kb + 16 * t + 8 * h), sf[t], dqacc[d]);
+            dqacc[d] = E::mma(ld8<T>(sKt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h)),
+                              sf[t], dqacc[d]);
       }
     }
   }
@@ -657,7 +674,8 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) float sOff[2][BM];
   __shared__ __attribute__((aligned(16))) float sDel[2][BM];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably wave-uniform
   const int N = p.N, D = p.D, org = p.org, nblk = p.nblk;
   const bool causal = p.causal != 0;
   const int npre = p.num_prefix;
@@ -796,8 +814,9 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
         for (int d = 0; d < ND; ++d)
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            dvacc[d] = E::mma(ld8<T>(sDt[buf] + (32 * d + n) * LDT + 32 * qb + 16 * t + 8 * h), pf[t], dvacc[d]);
-            dkacc[d] = E::mma(ld8<T>(sQt[buf] + (32 * d + n) * LDT + 32 * qb + 16 * t + 8 * h), sf[t], dkacc[d]);
+            const int off = (32 * d + n) * LDT + tchunk<BM>(32 * d + n, 32 * qb + 16 * t + 8 * h);
+            dvacc[d] = E::mma(ld8<T>(sDt[buf] + off), pf[t], dvacc[d]);
+            dkacc[d] = E::mma(ld8<T>(sQt[buf] + off), sf[t], dkacc[d]);
           }
       }
     }

@@ -95,6 +95,8 @@ def _base_args(variant: int, q: torch.Tensor, is_causal: bool, sm_scale: float, 
 
 
 def _launch(fn: str, a, device: torch.device) -> None:
+    if a.B * a.H * a.N == 0:
+        return  # empty problem: nothing to compute (data pointers may be NULL)
     with torch.cuda.device(device):
         _lib.call(fn, a, torch.cuda.current_stream(device).cuda_stream)
 
