@@ -47,7 +47,9 @@ def make_args(_lib, w, bufs, variant):
 
 def cpu_baseline(w, target_s: float):
     """The reference math path (oracle/math_path.py) on the host CPU, on a
-    bounded sample of the workload: the first B' batch rows."""
+    bounded sample of the workload: the first B' batch rows (all of them when
+    one pass fits in a third of the time budget), repeated for about
+    target_s seconds."""
     import torch
 
     from oracle import math_path
@@ -55,17 +57,25 @@ def cpu_baseline(w, target_s: float):
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    sample = w.with_(B=max(1, min(w.B, 2)))
-    q, k, v, do = wl.make_inputs(sample)
-    t0 = time.perf_counter()
-    math_path.fwd_bwd(q, k, v, do, sample.sm_scale, softmax=w.softmax, is_causal=w.causal)
-    first = time.perf_counter() - t0
-    reps = max(1, min(5, int(target_s / max(first, 1e-3))))
+
+    def one(sample):
+        q, k, v, do = wl.make_inputs(sample)
+        t0 = time.perf_counter()
+        math_path.fwd_bwd(q, k, v, do, sample.sm_scale, softmax=w.softmax, is_causal=w.causal)
+        return time.perf_counter() - t0, (q, k, v, do)
+
+    sample = w.with_(B=1)
+    first, _ = one(sample)  # warm-up and size probe
+    b = max(1, min(w.B, int((target_s / 3.0) / max(first, 1e-4))))
+    sample = w.with_(B=b)
+    _, (q, k, v, do) = one(sample)
     times = []
-    for _ in range(reps):
+    t_end = time.perf_counter() + target_s
+    while time.perf_counter() < t_end or len(times) < 3:
         t0 = time.perf_counter()
         math_path.fwd_bwd(q, k, v, do, sample.sm_scale, softmax=w.softmax, is_causal=w.causal)
         times.append(time.perf_counter() - t0)
+    reps = len(times)
     med = statistics.median(times)
     return {
         "value": round(sample.flops_fwd_bwd() / med / 1e12, 6),
@@ -75,9 +85,21 @@ def cpu_baseline(w, target_s: float):
         "sample": (
             f"reference math path restated in torch fp32 on CPU (augmented-dimension SDPA + autograd, "
             f"test_equivalence.py:9-33), fwd+bwd of B={sample.B} of {w.B} (H={w.H}, N={w.N}, D={w.D}); "
-            f"median of {reps} reps = {med * 1e3:.1f} ms after 1 warm-up"
+            f"median of {reps} reps = {med * 1e3:.1f} ms ({sum(times):.1f} s of CPU work) after a warm-up"
         ),
     }
+
+
+def measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` on `workload`, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/hbm_traffic.json,
+    calibrated on a copy kernel of known size); None if not profiled."""
+    path = os.path.join(REPO, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(workload, {}).get(kernel)
+    except (OSError, ValueError):
+        return None
 
 
 def main() -> int:
@@ -205,7 +227,7 @@ def main() -> int:
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": round(achieved / peak, 5),
-            "traffic": None,
+            "traffic": measured_traffic(w.name, dom),
         },
     }
     if not args.no_cpu_baseline:

@@ -168,6 +168,47 @@ __device__ inline int tchunk(int feat, int p8) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Combine a lane's value with the one of lane l ^ 32 (v_permlane32_swap: a
+// VALU op, no LDS round trip).  Both halves receive the same result.
+__device__ inline float xhalf_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float xhalf_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Sum over aligned groups of G consecutive lanes (G in {1, 2, 4, 8, 16}) with
+// DPP lane moves; every lane of a group receives the group sum.
+template <int G>
+__device__ inline float group_sum(float x) {
+  if constexpr (G >= 2) x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+  if constexpr (G >= 4) x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+  if constexpr (G >= 8) x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));
+  if constexpr (G >= 16) x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));
+  static_assert(G <= 16, "group_sum supports groups of at most 16 lanes");
+  return x;
+}
+
+// Pairwise (tree) reductions of the 16 accumulator values of a lane.
+__device__ inline float tree_sum16(const float v[16]) {
+  float a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = v[i] + v[i + 8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] += a[i + 4];
+  return (a[0] + a[2]) + (a[1] + a[3]);
+}
+__device__ inline float tree_max16(const f32x16_t& v) {
+  float a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = fmaxf(v[i], v[i + 8]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = fmaxf(a[i], a[i + 4]);
+  return fmaxf(fmaxf(a[0], a[2]), fmaxf(a[1], a[3]));
+}
+
 __device__ inline f32x16_t zero16() {
   f32x16_t z = {};
   return z;
@@ -271,18 +312,16 @@ struct Tile {
     }
   }
 
-  // nrm[row] = 0.5 * ||row||^2 in fp32 (from the input-dtype values).
-  __device__ inline void store_halfnorm(float* nrm, int tid) const {
+  // nrm[row] = sign * 0.5 * ||row||^2 in fp32 (from the input-dtype values).
+  __device__ inline void store_halfnorm(float* nrm, int tid, float sign) const {
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int u = tid + j * NT;
       const int rp = u / CPR, dc = u % CPR;
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        float s = sumsq8<T>(r[j][e]);
-#pragma unroll
-        for (int m = 1; m < CPR; m <<= 1) s += __shfl_xor(s, m);
-        if (dc == 0 && u < UNITS) nrm[2 * rp + e] = 0.5f * s;
+        const float s = group_sum<CPR>(sumsq8<T>(r[j][e]));
+        if (dc == 0 && u < UNITS) nrm[2 * rp + e] = (0.5f * sign) * s;
       }
     }
   }
@@ -302,28 +341,65 @@ __device__ inline void decode_wg(int ngrp, bool reverse, int& bh, int& grp) {
   grp = reverse ? (ngrp - 1 - j) : j;
 }
 
+// Visibility of a 32x32 (query block, key block) pair: `any` if at least one
+// pair (i, j) is visible, `full` if every pair is (no element mask needed).
+// Block starts below 0 hold padding tokens, which are never visible.
+__device__ inline bool blk_any(int q0, int k0, bool causal, int npre) {
+  return q0 + 31 >= 0 && k0 + 31 >= 0 && (!causal || k0 <= q0 + 31 || k0 < npre);
+}
+__device__ inline bool blk_full(int q0, int k0, bool causal, int npre) {
+  return q0 >= 0 && k0 >= 0 && (!causal || k0 + 31 <= q0 || k0 + 31 < npre);
+}
+__device__ inline bool elem_vis(int i, int j, bool causal, int npre) {
+  return i >= 0 && j >= 0 && (!causal || j <= i || j < npre);
+}
+
+// Per-slot values of a 32-entry fp32 LDS vector for the C layout rows of lane
+// half h: out[i] = v[crow(i, h)] (four 16-byte reads).
+__device__ inline f32x16_t ld_rows16(const float* v, int h) {
+  f32x16_t r;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const f32x4_t x = *reinterpret_cast<const f32x4_t*>(v + 8 * g + 4 * h);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[4 * g + e] = x[e];
+  }
+  return r;
+}
+
+__device__ inline f32x16_t splat16(float x) {
+  f32x16_t r;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r[i] = x;
+  return r;
+}
+
 // ---------------------------------------------------------------------------
-// Forward.  One wave owns 32 queries (one block); a work-group owns W
-// consecutive blocks and streams BN-key tiles of K (row-major) and V
-// (transposed) through double-buffered LDS.  O^T = V^T . P^T on MFMA.
+// Forward.  A wave owns QPW consecutive 32-query blocks, a work-group W
+// waves; BN-key tiles of K (row-major), V (transposed) and -0.5||k||^2 stream
+// through double-buffered LDS.  Per 32-key block the wave reads the K, V^T
+// fragments and key norms once and reuses them for its QPW query blocks:
+//   S^T = K Q^T (accumulator initialised with -0.5||k||^2),
+//   P   = exp2(c S^T - m) with a lazily raised running max m,
+//   O^T += V^T P^T.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int BN, bool SOFTMAX>
+template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX>
 __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
-  constexpr int NT = 64 * W, KB = BN / 32, KS = DP / 16, ND = DP / 32;
+  constexpr int NT = 64 * W, KB = BN / 32, KS = DP / 16, ND = DP / 32, GB = W * QPW;
   constexpr int LDR = DP + E::PAD, LDT = BN + E::PAD;
   __shared__ __attribute__((aligned(16))) T sK[2][BN * LDR];
   __shared__ __attribute__((aligned(16))) T sVt[2][DP * LDT];
   __shared__ __attribute__((aligned(16))) float sKn[2][BN];
 
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably wave-uniform
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int N = p.N, D = p.D, org = p.org, nblk = p.nblk;
   const bool causal = p.causal != 0;
   const int npre = p.num_prefix;
   const float c = p.c;
-  const int ngrp = (nblk + W - 1) / W;
+  const int ngrp = (nblk + GB - 1) / GB;
   int bh, grp;
   decode_wg(ngrp, causal, bh, grp);
   const int b = bh / p.H, hh = bh - b * p.H;
@@ -332,13 +408,10 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   const T* V = reinterpret_cast<const T*>(p.v) + b * p.sv[0] + hh * p.sv[1];
   T* O = reinterpret_cast<T*>(const_cast<void*>(p.o)) + b * p.so[0] + hh * p.so[1];
 
-  const int blk0 = nblk - (ngrp - grp) * W;
-  const int qblk = blk0 + wave;
-  const bool wave_on = qblk >= 0;
-  const int q0 = org + 32 * qblk;
-  const int qtok = q0 + n;
-  const bool qvalid = wave_on && qtok >= 0;
-  const int wg_qlast = org + 32 * (blk0 + W) - 1;
+  const int blk0 = nblk - (ngrp - grp) * GB;
+  const int qblk0 = blk0 + wave * QPW;            // first query block of this wave
+  const bool wave_on = qblk0 + QPW - 1 >= 0;      // its last block holds real queries
+  const int wg_qlast = org + 32 * (blk0 + GB) - 1;
   int hi = causal ? max(wg_qlast + 1, npre) : N;
   hi = min(hi, N);
   const int nkt_all = (nblk + KB - 1) / KB;
@@ -346,24 +419,36 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   const int last_blk = (hi - 1 - org) >> 5;
   const int nkt = (last_blk + kshift) / KB + 1;
 
-  frag qf[KS];
+  int q0[QPW], qtok[QPW];
+  frag qf[QPW][KS];
+  float qoff[QPW];
 #pragma unroll
-  for (int t = 0; t < KS; ++t)
-    qf[t] = (qvalid && 16 * t + 8 * h < D) ? ld8<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h) : zero_frag<T>();
-  float qoff = 0.f;
-  if constexpr (!SOFTMAX) {
-    float s = 0.f;
+  for (int j = 0; j < QPW; ++j) {
+    q0[j] = org + 32 * (qblk0 + j);
+    qtok[j] = q0[j] + n;
+    const bool ok = wave_on && qtok[j] >= 0;
 #pragma unroll
-    for (int t = 0; t < KS; ++t) s += sumsq8<T>(qf[t]);
-    s += __shfl_xor(s, 32);
-    qoff = c * 0.5f * s;
+    for (int t = 0; t < KS; ++t)
+      qf[j][t] = (ok && 16 * t + 8 * h < D) ? ld8<T>(Q + (int64_t)qtok[j] * p.sq[2] + 16 * t + 8 * h) : zero_frag<T>();
+    qoff[j] = 0.f;
+    if constexpr (!SOFTMAX) {
+      float s = 0.f;
+#pragma unroll
+      for (int t = 0; t < KS; ++t) s += sumsq8<T>(qf[j][t]);
+      s = xhalf_sum(s);
+      qoff[j] = c * 0.5f * s;
+    }
   }
 
-  f32x16_t oacc[ND];
+  f32x16_t oacc[QPW][ND];
+  float m_run[QPW], l_run[QPW];
 #pragma unroll
-  for (int d = 0; d < ND; ++d) oacc[d] = zero16();
-  float m_run = -__builtin_inff();
-  float l_run = 0.f;
+  for (int j = 0; j < QPW; ++j) {
+#pragma unroll
+    for (int d = 0; d < ND; ++d) oacc[j][d] = zero16();
+    m_run[j] = -__builtin_inff();
+    l_run[j] = 0.f;
+  }
 
   Tile<T, BN, DP, NT> tk, tv;
   {
@@ -374,7 +459,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   for (int kt = 0; kt < nkt; ++kt) {
     const int buf = kt & 1;
     tk.template store_rows<LDR>(sK[buf], tid);
-    tk.store_halfnorm(sKn[buf], tid);
+    tk.store_halfnorm(sKn[buf], tid, -1.f);
     tv.template store_trans<LDT>(sVt[buf], tid);
     __syncthreads();
     if (kt + 1 < nkt) {
@@ -382,113 +467,109 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
       tk.load(K, p.sk[2], tok1, N, D, tid);
       tv.load(V, p.sv[2], tok1, N, D, tid);
     }
-    if (wave_on) {
-      const int kblk0 = kt * KB - kshift;
-      f32x16_t s[KB];
-      bool act[KB];
+    if (!wave_on) continue;
+    const int kblk0 = kt * KB - kshift;
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        const int k0 = org + 32 * (kblk0 + kb);
-        act[kb] = (kblk0 + kb >= 0) && (!causal || k0 <= q0 + 31 || k0 < npre);
-        if (act[kb]) {
-          const bool full = k0 >= 0 && q0 >= 0 && (!causal || k0 + 31 <= q0 || k0 + 31 < npre);
-          const float* kn = sKn[buf] + 32 * kb + 4 * h;
+    for (int kb = 0; kb < KB; ++kb) {
+      const int k0 = org + 32 * (kblk0 + kb);
+      bool act[QPW];
+      bool any = false;
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(kn + 8 * g);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) s[kb][4 * g + e] = -v4[e];
-          }
-#pragma unroll
-          for (int t = 0; t < KS; ++t)
-            s[kb] = E::mma(ld8<T>(sK[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h), qf[t], s[kb]);
-          if (!full) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const int j = k0 + crow(i, h);
-              const bool vis = j >= 0 && qtok >= 0 && (!causal || j <= qtok || j < npre);
-              if (!vis) s[kb][i] = -__builtin_inff();
-            }
-          }
-        }
+      for (int j = 0; j < QPW; ++j) {
+        act[j] = blk_any(q0[j], k0, causal, npre);
+        any = any || act[j];
       }
-      float moff;
-      if constexpr (SOFTMAX) {
-        float mx = -__builtin_inff();
+      if (!any) continue;
+      frag kA[KS];
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-          if (act[kb]) {
+      for (int t = 0; t < KS; ++t) kA[t] = ld8<T>(sK[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h);
+      const f32x16_t kinit = ld_rows16(sKn[buf] + 32 * kb, h);
+      frag pf[QPW][2];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-          }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mt = mx * c;
-        if (__any(mt > m_run + kTau)) {
-          const float mnew = fmaxf(m_run, mt);
-          const float alpha = (mnew == -__builtin_inff()) ? 1.f : fast_exp2(m_run - mnew);
-          l_run *= alpha;
+      for (int j = 0; j < QPW; ++j) {
+        if (!act[j]) continue;
+        f32x16_t s = kinit;
 #pragma unroll
-          for (int d = 0; d < ND; ++d) oacc[d] *= alpha;
-          m_run = mnew;
+        for (int t = 0; t < KS; ++t) s = E::mma(kA[t], qf[j][t], s);
+        if (!blk_full(q0[j], k0, causal, npre)) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            if (!elem_vis(qtok[j], k0 + crow(i, h), causal, npre)) s[i] = -__builtin_inff();
         }
-        moff = (m_run == -__builtin_inff()) ? 0.f : m_run;
-      } else {
-        moff = qoff;
-      }
+        float moff;
+        if constexpr (SOFTMAX) {
+          const float mx = xhalf_max(tree_max16(s));
+          const float mt = mx * c;
+          if (__any(mt > m_run[j] + kTau)) {
+            const float mnew = fmaxf(m_run[j], mt);
+            const float alpha = (mnew == -__builtin_inff()) ? 1.f : fast_exp2(m_run[j] - mnew);
+            l_run[j] *= alpha;
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        if (!act[kb]) continue;
-        frag pf[2];
+            for (int d = 0; d < ND; ++d) oacc[j][d] *= alpha;
+            m_run[j] = mnew;
+          }
+          moff = (m_run[j] == -__builtin_inff()) ? 0.f : m_run[j];
+        } else {
+          moff = qoff[j];
+        }
+        float pv[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float pv = fast_exp2(fmaf(s[kb][i], c, -moff));
-          if constexpr (SOFTMAX) l_run += pv;
-          pf[i >> 3][i & 7] = (T)pv;
+          pv[i] = fast_exp2(fmaf(s[i], c, -moff));
+          pf[j][i >> 3][i & 7] = (T)pv[i];
         }
-#pragma unroll
-        for (int d = 0; d < ND; ++d)
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-            oacc[d] = E::mma(ld8<T>(sVt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h)),
-                             pf[t], oacc[d]);
+        if constexpr (SOFTMAX) l_run[j] += tree_sum16(pv);
       }
-    }
-  }
-
-  if (wave_on) {
-    float lsum = l_run;
-    if constexpr (SOFTMAX) lsum += __shfl_xor(lsum, 32);
-    const float inv = SOFTMAX ? 1.f / lsum : 1.f;
-    if (qvalid) {
-      T* orow = O + (int64_t)qtok * p.so[2];
 #pragma unroll
       for (int d = 0; d < ND; ++d)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int dd = 32 * d + 8 * g + 4 * h;
-          if (dd < D) {
-            float v4[4];
+        for (int t = 0; t < 2; ++t) {
+          const frag vA = ld8<T>(sVt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v4[e] = oacc[d][4 * g + e] * inv;
-            st4f<T>(orow + dd, v4);
-          }
+          for (int j = 0; j < QPW; ++j)
+            if (act[j]) oacc[j][d] = E::mma(vA, pf[j][t], oacc[j][d]);
         }
-      if (SOFTMAX && h == 0) p.lse[(int64_t)bh * N + qtok] = m_run + __log2f(lsum);
     }
+  }
+
+  if (!wave_on) return;
+#pragma unroll
+  for (int j = 0; j < QPW; ++j) {
+    float lsum = l_run[j];
+    if constexpr (SOFTMAX) lsum = xhalf_sum(lsum);
+    const float inv = SOFTMAX ? 1.f / lsum : 1.f;
+    if (qtok[j] < 0) continue;
+    T* orow = O + (int64_t)qtok[j] * p.so[2];
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dd = 32 * d + 8 * g + 4 * h;
+        if (dd < D) {
+          float v4[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v4[e] = oacc[j][d][4 * g + e] * inv;
+          st4f<T>(orow + dd, v4);
+        }
+      }
+    if (SOFTMAX && h == 0) p.lse[(int64_t)bh * N + qtok[j]] = m_run[j] + __log2f(lsum);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Backward, query-stationary: dQ.  Also produces, per query, Delta =
-// rowsum(O*dO) (softmax) or the norm offset c*0.5*||q||^2 written to the lse
-// workspace (non-softmax), both consumed by the dK/dV kernel launched next.
-// K (row-major and transposed), V (row-major) stream through LDS.
+// Backward, query-stationary: dQ.  A wave owns QPW query blocks.  Also
+// produces, per query, Delta = rowsum(O*dO) (softmax) or the norm offset
+// c*0.5*||q||^2 (non-softmax, written to the lse workspace), both consumed by
+// the dK/dV kernel launched next.  K (row-major and transposed), V
+// (row-major) and -0.5||k||^2 stream through LDS.
+//   S^T = K Q^T (init -0.5||k||^2), P = exp2(c S^T - L),
+//   dP^T = V dO^T (init -Delta), dS = P dP^T, dQ^T += K^T dS^T.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int BN, bool SOFTMAX>
+template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX>
 __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
-  constexpr int NT = 64 * W, KB = BN / 32, KS = DP / 16, ND = DP / 32;
+  constexpr int NT = 64 * W, KB = BN / 32, KS = DP / 16, ND = DP / 32, GB = W * QPW;
   constexpr int LDR = DP + E::PAD, LDT = BN + E::PAD;
   __shared__ __attribute__((aligned(16))) T sK[2][BN * LDR];
   __shared__ __attribute__((aligned(16))) T sKt[2][DP * LDT];
@@ -496,12 +577,12 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) float sKn[2][BN];
 
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably wave-uniform
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int N = p.N, D = p.D, org = p.org, nblk = p.nblk;
   const bool causal = p.causal != 0;
   const int npre = p.num_prefix;
   const float c = p.c;
-  const int ngrp = (nblk + W - 1) / W;
+  const int ngrp = (nblk + GB - 1) / GB;
   int bh, grp;
   decode_wg(ngrp, causal, bh, grp);
   const int b = bh / p.H, hh = bh - b * p.H;
@@ -512,13 +593,10 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   const T* dO = reinterpret_cast<const T*>(p.dout) + b * p.sdo[0] + hh * p.sdo[1];
   T* dQ = reinterpret_cast<T*>(p.dq) + b * p.sdq[0] + hh * p.sdq[1];
 
-  const int blk0 = nblk - (ngrp - grp) * W;
-  const int qblk = blk0 + wave;
-  const bool wave_on = qblk >= 0;
-  const int q0 = org + 32 * qblk;
-  const int qtok = q0 + n;
-  const bool qvalid = wave_on && qtok >= 0;
-  const int wg_qlast = org + 32 * (blk0 + W) - 1;
+  const int blk0 = nblk - (ngrp - grp) * GB;
+  const int qblk0 = blk0 + wave * QPW;
+  const bool wave_on = qblk0 + QPW - 1 >= 0;
+  const int wg_qlast = org + 32 * (blk0 + GB) - 1;
   int hi = causal ? max(wg_qlast + 1, npre) : N;
   hi = min(hi, N);
   const int nkt_all = (nblk + KB - 1) / KB;
@@ -526,40 +604,53 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   const int last_blk = (hi - 1 - org) >> 5;
   const int nkt = (last_blk + kshift) / KB + 1;
 
-  frag qf[KS], df[KS];
+  int q0[QPW], qtok[QPW];
+  frag qf[QPW][KS], df[QPW][KS];
+  float off[QPW];
+  f32x16_t ndel[QPW];  // -Delta broadcast: the dP accumulator's initial value
 #pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    const bool ok = qvalid && 16 * t + 8 * h < D;
-    qf[t] = ok ? ld8<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h) : zero_frag<T>();
-    df[t] = ok ? ld8<T>(dO + (int64_t)qtok * p.sdo[2] + 16 * t + 8 * h) : zero_frag<T>();
-  }
-  float off, dlt;
-  if constexpr (SOFTMAX) {
-    float s = 0.f;
+  for (int j = 0; j < QPW; ++j) {
+    q0[j] = org + 32 * (qblk0 + j);
+    qtok[j] = q0[j] + n;
+    const bool qvalid = wave_on && qtok[j] >= 0;
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
       const bool ok = qvalid && 16 * t + 8 * h < D;
-      const frag of = ok ? ld8<T>(Og + (int64_t)qtok * p.so[2] + 16 * t + 8 * h) : zero_frag<T>();
-      s += dot8<T>(of, df[t]);
+      qf[j][t] = ok ? ld8<T>(Q + (int64_t)qtok[j] * p.sq[2] + 16 * t + 8 * h) : zero_frag<T>();
+      df[j][t] = ok ? ld8<T>(dO + (int64_t)qtok[j] * p.sdo[2] + 16 * t + 8 * h) : zero_frag<T>();
     }
-    s += __shfl_xor(s, 32);
-    dlt = s;
-    off = qvalid ? p.lse[(int64_t)bh * N + qtok] : 0.f;
-    if (qvalid && h == 0) p.delta[(int64_t)bh * N + qtok] = dlt;
-  } else {
-    float s = 0.f;
+    float dlt = 0.f;
+    if constexpr (SOFTMAX) {
+      float s = 0.f;
 #pragma unroll
-    for (int t = 0; t < KS; ++t) s += sumsq8<T>(qf[t]);
-    s += __shfl_xor(s, 32);
-    off = c * 0.5f * s;
-    dlt = 0.f;
-    if (qvalid && h == 0) p.lse[(int64_t)bh * N + qtok] = off;
+      for (int t = 0; t < KS; ++t) {
+        const bool ok = qvalid && 16 * t + 8 * h < D;
+        const frag of = ok ? ld8<T>(Og + (int64_t)qtok[j] * p.so[2] + 16 * t + 8 * h) : zero_frag<T>();
+        s += dot8<T>(of, df[j][t]);
+      }
+      s = xhalf_sum(s);
+      dlt = s;
+      off[j] = qvalid ? p.lse[(int64_t)bh * N + qtok[j]] : 0.f;
+      if (qvalid && h == 0) p.delta[(int64_t)bh * N + qtok[j]] = dlt;
+    } else {
+      float s = 0.f;
+#pragma unroll
+      for (int t = 0; t < KS; ++t) s += sumsq8<T>(qf[j][t]);
+      s = xhalf_sum(s);
+      off[j] = c * 0.5f * s;
+      if (qvalid && h == 0) p.lse[(int64_t)bh * N + qtok[j]] = off[j];
+    }
+    ndel[j] = splat16(-dlt);
   }
 
-  f32x16_t dqacc[ND];
+  f32x16_t dqacc[QPW][ND];
+  float rsum[QPW];
 #pragma unroll
-  for (int d = 0; d < ND; ++d) dqacc[d] = zero16();
-  float rsum = 0.f;
+  for (int j = 0; j < QPW; ++j) {
+#pragma unroll
+    for (int d = 0; d < ND; ++d) dqacc[j][d] = zero16();
+    rsum[j] = 0.f;
+  }
 
   Tile<T, BN, DP, NT> tk, tv;
   {
@@ -571,7 +662,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
     const int buf = kt & 1;
     tk.template store_rows<LDR>(sK[buf], tid);
     tk.template store_trans<LDT>(sKt[buf], tid);
-    tk.store_halfnorm(sKn[buf], tid);
+    tk.store_halfnorm(sKn[buf], tid, -1.f);
     tv.template store_rows<LDR>(sV[buf], tid);
     __syncthreads();
     if (kt + 1 < nkt) {
@@ -579,93 +670,107 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
       tk.load(K, p.sk[2], tok1, N, D, tid);
       tv.load(V, p.sv[2], tok1, N, D, tid);
     }
-    if (wave_on) {
-      const int kblk0 = kt * KB - kshift;
+    if (!wave_on) continue;
+    const int kblk0 = kt * KB - kshift;
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        const int k0 = org + 32 * (kblk0 + kb);
-        const bool act = (kblk0 + kb >= 0) && (!causal || k0 <= q0 + 31 || k0 < npre);
-        if (!act) continue;
-        const bool full = k0 >= 0 && q0 >= 0 && (!causal || k0 + 31 <= q0 || k0 + 31 < npre);
-        f32x16_t s, dp = zero16();
-        const float* kn = sKn[buf] + 32 * kb + 4 * h;
+    for (int kb = 0; kb < KB; ++kb) {
+      const int k0 = org + 32 * (kblk0 + kb);
+      bool act[QPW];
+      bool any = false;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(kn + 8 * g);
+      for (int j = 0; j < QPW; ++j) {
+        act[j] = blk_any(q0[j], k0, causal, npre);
+        any = any || act[j];
+      }
+      if (!any) continue;
+      frag kA[KS], vA[KS];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) s[4 * g + e] = -v4[e];
-        }
+      for (int t = 0; t < KS; ++t) {
+        kA[t] = ld8<T>(sK[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h);
+        vA[t] = ld8<T>(sV[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h);
+      }
+      const f32x16_t kinit = ld_rows16(sKn[buf] + 32 * kb, h);
+      frag sf[QPW][2];
+#pragma unroll
+      for (int j = 0; j < QPW; ++j) {
+        if (!act[j]) continue;
+        f32x16_t s = kinit, dp = ndel[j];
 #pragma unroll
         for (int t = 0; t < KS; ++t) {
-          s = E::mma(ld8<T>(sK[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h), qf[t], s);
-          dp = E::mma(ld8<T>(sV[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h), df[t], dp);
+          s = E::mma(kA[t], qf[j][t], s);
+          dp = E::mma(vA[t], df[j][t], dp);
         }
-        if (!full) {
+        if (!blk_full(q0[j], k0, causal, npre)) {
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int j = k0 + crow(i, h);
-            const bool vis = j >= 0 && qtok >= 0 && (!causal || j <= qtok || j < npre);
-            if (!vis) s[i] = -__builtin_inff();
-          }
+          for (int i = 0; i < 16; ++i)
+            if (!elem_vis(qtok[j], k0 + crow(i, h), causal, npre)) s[i] = -__builtin_inff();
         }
-        frag sf[2];
+        float ds[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float pv = fast_exp2(fmaf(s[i], c, -off));
-          const float ds = pv * (dp[i] - dlt);
-          if constexpr (!SOFTMAX) rsum += ds;
-          sf[i >> 3][i & 7] = (T)ds;
+          ds[i] = fast_exp2(fmaf(s[i], c, -off[j])) * dp[i];
+          sf[j][i >> 3][i & 7] = (T)ds[i];
         }
-#pragma unroll
-        for (int d = 0; d < ND; ++d)
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-            dqacc[d] = E::mma(ld8<T>(sKt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h)),
-                              sf[t], dqacc[d]);
+        if constexpr (!SOFTMAX) rsum[j] += tree_sum16(ds);
       }
-    }
-  }
-
-  if (wave_on) {
-    float rs = 0.f;
-    if constexpr (!SOFTMAX) rs = rsum + __shfl_xor(rsum, 32);
-    if (qvalid) {
-      const float g2 = 2.f * p.gamma;
-      T* drow = dQ + (int64_t)qtok * p.sdq[2];
-      const T* qrow = Q + (int64_t)qtok * p.sq[2];
 #pragma unroll
       for (int d = 0; d < ND; ++d)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int dd = 32 * d + 8 * g + 4 * h;
-          if (dd < D) {
-            float v4[4];
-            if constexpr (SOFTMAX) {
+        for (int t = 0; t < 2; ++t) {
+          const frag ktA = ld8<T>(sKt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h));
 #pragma unroll
-              for (int e = 0; e < 4; ++e) v4[e] = g2 * dqacc[d][4 * g + e];
-            } else {
-              float q4[4];
-              ld4f<T>(qrow + dd, q4);
-#pragma unroll
-              for (int e = 0; e < 4; ++e) v4[e] = g2 * (dqacc[d][4 * g + e] - rs * q4[e]);
-            }
-            st4f<T>(drow + dd, v4);
-          }
+          for (int j = 0; j < QPW; ++j)
+            if (act[j]) dqacc[j][d] = E::mma(ktA, sf[j][t], dqacc[j][d]);
         }
     }
+  }
+
+  if (!wave_on) return;
+  const float g2 = 2.f * p.gamma;
+#pragma unroll
+  for (int j = 0; j < QPW; ++j) {
+    float rs = 0.f;
+    if constexpr (!SOFTMAX) rs = xhalf_sum(rsum[j]);
+    if (qtok[j] < 0) continue;
+    T* drow = dQ + (int64_t)qtok[j] * p.sdq[2];
+    const T* qrow = Q + (int64_t)qtok[j] * p.sq[2];
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dd = 32 * d + 8 * g + 4 * h;
+        if (dd < D) {
+          float v4[4];
+          if constexpr (SOFTMAX) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v4[e] = g2 * dqacc[j][d][4 * g + e];
+          } else {
+            float q4[4];
+            ld4f<T>(qrow + dd, q4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v4[e] = g2 * (dqacc[j][d][4 * g + e] - rs * q4[e]);
+          }
+          st4f<T>(drow + dd, v4);
+        }
+      }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Backward, key-stationary: dK and dV.  One wave owns 32 keys (K and V held in
-// registers); BM-query tiles of Q and dO (row-major and transposed) plus the
-// per-query offset (L, or c*0.5*||q||^2) and Delta stream through LDS.
+// Backward, key-stationary: dK and dV.  A wave owns KPW key blocks (K and V
+// fragments in registers); BM-query tiles of Q and dO (row-major and
+// transposed), the per-query offset -L/c (or -0.5||q||^2) and -Delta stream
+// through LDS.  Per 32-query block the wave reads the Q, dO fragments and the
+// offsets once and reuses them for its KPW key blocks:
+//   S = Q K^T (init -L/c), P = exp2(c S - c*0.5||k||^2),
+//   dP = dO V^T (init -Delta), dS = P dP,
+//   dV^T += dO^T P, dK^T += Q^T dS, colsum += sum_i dS.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int BM, bool SOFTMAX>
+template <typename T, int DP, int W, int KPW, int BM, bool SOFTMAX>
 __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
-  constexpr int NT = 64 * W, QB = BM / 32, KS = DP / 16, ND = DP / 32;
+  constexpr int NT = 64 * W, QB = BM / 32, KS = DP / 16, ND = DP / 32, GB = W * KPW;
   constexpr int LDR = DP + E::PAD, LDT = BM + E::PAD;
   __shared__ __attribute__((aligned(16))) T sQ[2][BM * LDR];
   __shared__ __attribute__((aligned(16))) T sQt[2][DP * LDT];
@@ -675,12 +780,13 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) float sDel[2][BM];
 
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably wave-uniform
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int N = p.N, D = p.D, org = p.org, nblk = p.nblk;
   const bool causal = p.causal != 0;
   const int npre = p.num_prefix;
   const float c = p.c;
-  const int ngrp = (nblk + W - 1) / W;
+  const float inv_c = 1.f / c;
+  const int ngrp = (nblk + GB - 1) / GB;
   int bh, grp;
   decode_wg(ngrp, false, bh, grp);
   const int b = bh / p.H, hh = bh - b * p.H;
@@ -693,36 +799,41 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   const float* offg = p.lse + (int64_t)bh * N;
   const float* delg = SOFTMAX ? p.delta + (int64_t)bh * N : nullptr;
 
-  const int blk0 = nblk - (ngrp - grp) * W;
-  const int kblk = blk0 + wave;
-  const bool wave_on = kblk >= 0;
-  const int k0 = org + 32 * kblk;
-  const int ktok = k0 + n;
-  const bool kvalid = wave_on && ktok >= 0;
+  const int blk0 = nblk - (ngrp - grp) * GB;
+  const int kblk0 = blk0 + wave * KPW;
+  const bool wave_on = kblk0 + KPW - 1 >= 0;
 
-  frag kf[KS], vf[KS];
+  int k0[KPW], ktok[KPW];
+  frag kf[KPW][KS], vf[KPW][KS];
+  float nckn[KPW];  // -c * 0.5||k||^2
 #pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    const bool ok = kvalid && 16 * t + 8 * h < D;
-    kf[t] = ok ? ld8<T>(K + (int64_t)ktok * p.sk[2] + 16 * t + 8 * h) : zero_frag<T>();
-    vf[t] = ok ? ld8<T>(V + (int64_t)ktok * p.sv[2] + 16 * t + 8 * h) : zero_frag<T>();
-  }
-  float kn;
-  {
+  for (int j = 0; j < KPW; ++j) {
+    k0[j] = org + 32 * (kblk0 + j);
+    ktok[j] = k0[j] + n;
+    const bool kvalid = wave_on && ktok[j] >= 0;
     float s = 0.f;
 #pragma unroll
-    for (int t = 0; t < KS; ++t) s += sumsq8<T>(kf[t]);
-    s += __shfl_xor(s, 32);
-    kn = 0.5f * s;
+    for (int t = 0; t < KS; ++t) {
+      const bool ok = kvalid && 16 * t + 8 * h < D;
+      kf[j][t] = ok ? ld8<T>(K + (int64_t)ktok[j] * p.sk[2] + 16 * t + 8 * h) : zero_frag<T>();
+      vf[j][t] = ok ? ld8<T>(V + (int64_t)ktok[j] * p.sv[2] + 16 * t + 8 * h) : zero_frag<T>();
+      s += sumsq8<T>(kf[j][t]);
+    }
+    s = xhalf_sum(s);
+    nckn[j] = -c * 0.5f * s;
   }
 
-  f32x16_t dkacc[ND], dvacc[ND];
+  f32x16_t dkacc[KPW][ND], dvacc[KPW][ND];
+  float csum[KPW];
 #pragma unroll
-  for (int d = 0; d < ND; ++d) {
-    dkacc[d] = zero16();
-    dvacc[d] = zero16();
+  for (int j = 0; j < KPW; ++j) {
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+      dkacc[j][d] = zero16();
+      dvacc[j][d] = zero16();
+    }
+    csum[j] = 0.f;
   }
-  float csum = 0.f;
 
   // Query range: causal keys are seen by queries at or after them, except
   // prefix (register) keys, which every query sees.
@@ -741,8 +852,8 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
     if (tid < BM) {
       const int tok = tok0 + tid;
       const bool ok = tok >= 0 && tok < N;
-      offr = ok ? offg[tok] : 0.f;
-      if constexpr (SOFTMAX) delr = ok ? delg[tok] : 0.f;
+      offr = ok ? -offg[tok] * inv_c : 0.f;
+      if constexpr (SOFTMAX) delr = ok ? -delg[tok] : 0.f;
     }
   };
   load_tile(qt_lo);
@@ -758,95 +869,97 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
     }
     __syncthreads();
     if (qt + 1 < nqt_all) load_tile(qt + 1);
-    if (wave_on) {
-      const int qblk0 = qt * QB - qshift;
+    if (!wave_on) continue;
+    const int qblk0 = qt * QB - qshift;
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        const int q0 = org + 32 * (qblk0 + qb);
-        const bool act = (qblk0 + qb >= 0) && (!causal || q0 + 31 >= k0 || k0 < npre);
-        if (!act) continue;
-        const bool full = q0 >= 0 && k0 >= 0 && (!causal || q0 >= k0 + 31 || k0 + 31 < npre);
-        f32x16_t s, dp = zero16();
+    for (int qb = 0; qb < QB; ++qb) {
+      const int q0 = org + 32 * (qblk0 + qb);
+      bool act[KPW];
+      bool any = false;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s[i] = -kn;
+      for (int j = 0; j < KPW; ++j) {
+        act[j] = blk_any(q0, k0[j], causal, npre);
+        any = any || act[j];
+      }
+      if (!any) continue;
+      frag qA[KS], dA[KS];
+#pragma unroll
+      for (int t = 0; t < KS; ++t) {
+        qA[t] = ld8<T>(sQ[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h);
+        dA[t] = ld8<T>(sD[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h);
+      }
+      const f32x16_t oinit = ld_rows16(sOff[buf] + 32 * qb, h);
+      f32x16_t dinit;
+      if constexpr (SOFTMAX) dinit = ld_rows16(sDel[buf] + 32 * qb, h);
+      else dinit = zero16();
+      frag pf[KPW][2], sf[KPW][2];
+#pragma unroll
+      for (int j = 0; j < KPW; ++j) {
+        if (!act[j]) continue;
+        f32x16_t s = oinit, dp = dinit;
 #pragma unroll
         for (int t = 0; t < KS; ++t) {
-          s = E::mma(ld8<T>(sQ[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h), kf[t], s);
-          dp = E::mma(ld8<T>(sD[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h), vf[t], dp);
+          s = E::mma(qA[t], kf[j][t], s);
+          dp = E::mma(dA[t], vf[j][t], dp);
         }
-        if (!full) {
+        if (!blk_full(q0, k0[j], causal, npre)) {
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int it = q0 + crow(i, h);
-            const bool vis = it >= 0 && ktok >= 0 && (!causal || ktok <= it || ktok < npre);
-            if (!vis) s[i] = -__builtin_inff();
-          }
+          for (int i = 0; i < 16; ++i)
+            if (!elem_vis(q0 + crow(i, h), ktok[j], causal, npre)) s[i] = -__builtin_inff();
         }
-        float offv[16], delv[16];
-        {
-          const float* po = sOff[buf] + 32 * qb + 4 * h;
-          const float* pd = sDel[buf] + 32 * qb + 4 * h;
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const f32x4_t o4 = *reinterpret_cast<const f32x4_t*>(po + 8 * g);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) offv[4 * g + e] = o4[e];
-            if constexpr (SOFTMAX) {
-              const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(pd + 8 * g);
-#pragma unroll
-              for (int e = 0; e < 4; ++e) delv[4 * g + e] = d4[e];
-            } else {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) delv[4 * g + e] = 0.f;
-            }
-          }
-        }
-        frag pf[2], sf[2];
+        float ds[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float pv = fast_exp2(fmaf(s[i], c, -offv[i]));
-          const float ds = pv * (dp[i] - delv[i]);
-          csum += ds;
-          pf[i >> 3][i & 7] = (T)pv;
-          sf[i >> 3][i & 7] = (T)ds;
+          const float pv = fast_exp2(fmaf(s[i], c, nckn[j]));
+          ds[i] = pv * dp[i];
+          pf[j][i >> 3][i & 7] = (T)pv;
+          sf[j][i >> 3][i & 7] = (T)ds[i];
         }
-#pragma unroll
-        for (int d = 0; d < ND; ++d)
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const int off = (32 * d + n) * LDT + tchunk<BM>(32 * d + n, 32 * qb + 16 * t + 8 * h);
-            dvacc[d] = E::mma(ld8<T>(sDt[buf] + off), pf[t], dvacc[d]);
-            dkacc[d] = E::mma(ld8<T>(sQt[buf] + off), sf[t], dkacc[d]);
-          }
+        csum[j] += tree_sum16(ds);
       }
-    }
-  }
-
-  if (wave_on) {
-    const float cs = csum + __shfl_xor(csum, 32);
-    if (kvalid) {
-      const float g2 = 2.f * p.gamma;
-      T* dkrow = dK + (int64_t)ktok * p.sdk[2];
-      T* dvrow = dV + (int64_t)ktok * p.sdv[2];
-      const T* krow = K + (int64_t)ktok * p.sk[2];
 #pragma unroll
       for (int d = 0; d < ND; ++d)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int dd = 32 * d + 8 * g + 4 * h;
-          if (dd < D) {
-            float k4[4], a4[4], b4[4];
-            ld4f<T>(krow + dd, k4);
+        for (int t = 0; t < 2; ++t) {
+          const int o = (32 * d + n) * LDT + tchunk<BM>(32 * d + n, 32 * qb + 16 * t + 8 * h);
+          const frag dtA = ld8<T>(sDt[buf] + o);
+          const frag qtA = ld8<T>(sQt[buf] + o);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              a4[e] = g2 * (dkacc[d][4 * g + e] - cs * k4[e]);
-              b4[e] = dvacc[d][4 * g + e];
+          for (int j = 0; j < KPW; ++j)
+            if (act[j]) {
+              dvacc[j][d] = E::mma(dtA, pf[j][t], dvacc[j][d]);
+              dkacc[j][d] = E::mma(qtA, sf[j][t], dkacc[j][d]);
             }
-            st4f<T>(dkrow + dd, a4);
-            st4f<T>(dvrow + dd, b4);
-          }
         }
     }
+  }
+
+  if (!wave_on) return;
+  const float g2 = 2.f * p.gamma;
+#pragma unroll
+  for (int j = 0; j < KPW; ++j) {
+    const float cs = xhalf_sum(csum[j]);
+    if (ktok[j] < 0) continue;
+    T* dkrow = dK + (int64_t)ktok[j] * p.sdk[2];
+    T* dvrow = dV + (int64_t)ktok[j] * p.sdv[2];
+    const T* krow = K + (int64_t)ktok[j] * p.sk[2];
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dd = 32 * d + 8 * g + 4 * h;
+        if (dd < D) {
+          float k4[4], a4[4], b4[4];
+          ld4f<T>(krow + dd, k4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            a4[e] = g2 * (dkacc[j][d][4 * g + e] - cs * k4[e]);
+            b4[e] = dvacc[j][d][4 * g + e];
+          }
+          st4f<T>(dkrow + dd, a4);
+          st4f<T>(dvrow + dd, b4);
+        }
+      }
   }
 }
 

@@ -2,12 +2,13 @@
 // -DRBF_ELEM_ID=0 (bf16), 1 (fp16) or 2 (fp32), so the three instantiation
 // sets build in parallel.
 //
-// Tile choices (tokens per LDS tile, waves per work-group) per head dim:
-//   fwd:  4 waves x 32 queries; BN = 64 keys (32 for fp32).
-//   dQ:   4 waves x 32 queries; BN = 64 keys for D <= 64, 32 for D = 128
-//         (three LDS tiles: K, K^T, V), 32 for fp32.
-//   dKdV: 4 waves x 32 keys; BM = 64 queries for D <= 64, 32 for D = 128
-//         (four LDS tiles: Q, Q^T, dO, dO^T), 32 for fp32.
+// A kernel configuration is (W waves per work-group, blocks of 32 tokens per
+// wave, LDS tile of streamed tokens).  Defaults per padded head dim DP are in
+// the *_default() functions; for bf16 a few alternatives are also compiled and
+// can be chosen with RBF_ATTN_FWD_CFG / RBF_ATTN_DQ_CFG / RBF_ATTN_DKDV_CFG
+// (an index into the candidate lists below) for tuning sweeps.
+#include <stdlib.h>
+
 #include "rbf_attn_kernels.h"
 #include "rbf_attn_launch.h"
 
@@ -26,49 +27,131 @@ typedef _Float16 Elt;
 typedef float Elt;
 #endif
 
-constexpr int kWaves = 4;
 constexpr bool kIsF32 = sizeof(Elt) == 4;
 
-inline unsigned grid_of(const Params& p) {
-  const int ngrp = (p.nblk + kWaves - 1) / kWaves;
+inline unsigned grid_of(const Params& p, int blocks_per_wg) {
+  const int ngrp = (p.nblk + blocks_per_wg - 1) / blocks_per_wg;
   return (unsigned)((long long)p.B * p.H * ngrp);
 }
 
-template <int DP, bool SM>
-hipError_t fwd(const Params& p, hipStream_t st) {
-  constexpr int BN = kIsF32 ? 32 : 64;
-  hipLaunchKernelGGL((rbf_fwd_kernel<Elt, DP, kWaves, BN, SM>), dim3(grid_of(p)), dim3(64 * kWaves), 0, st, p);
+template <int DP, bool SM, int W, int QPW, int BN>
+hipError_t fwd_cfg(const Params& p, hipStream_t st) {
+  hipLaunchKernelGGL((rbf_fwd_kernel<Elt, DP, W, QPW, BN, SM>), dim3(grid_of(p, W * QPW)), dim3(64 * W), 0, st, p);
   return hipGetLastError();
 }
 
-template <int DP, bool SM>
-hipError_t dq(const Params& p, hipStream_t st) {
-  constexpr int BN = (kIsF32 || DP > 64) ? 32 : 64;
-  hipLaunchKernelGGL((rbf_bwd_dq_kernel<Elt, DP, kWaves, BN, SM>), dim3(grid_of(p)), dim3(64 * kWaves), 0, st, p);
+template <int DP, bool SM, int W, int QPW, int BN>
+hipError_t dq_cfg(const Params& p, hipStream_t st) {
+  hipLaunchKernelGGL((rbf_bwd_dq_kernel<Elt, DP, W, QPW, BN, SM>), dim3(grid_of(p, W * QPW)), dim3(64 * W), 0, st,
+                     p);
   return hipGetLastError();
 }
 
-template <int DP, bool SM>
-hipError_t dkdv(const Params& p, hipStream_t st) {
-  constexpr int BM = (kIsF32 || DP > 64) ? 32 : 64;
-  hipLaunchKernelGGL((rbf_bwd_dkdv_kernel<Elt, DP, kWaves, BM, SM>), dim3(grid_of(p)), dim3(64 * kWaves), 0,
+template <int DP, bool SM, int W, int KPW, int BM>
+hipError_t dkdv_cfg(const Params& p, hipStream_t st) {
+  hipLaunchKernelGGL((rbf_bwd_dkdv_kernel<Elt, DP, W, KPW, BM, SM>), dim3(grid_of(p, W * KPW)), dim3(64 * W), 0,
                      st, p);
   return hipGetLastError();
 }
 
+int env_choice(const char* name) {
+  const char* s = getenv(name);
+  return s ? atoi(s) : -1;
+}
+
+// ---- defaults ------------------------------------------------------------
+template <int DP, bool SM>
+hipError_t fwd_default(const Params& p, hipStream_t st) {
+  if constexpr (kIsF32) return fwd_cfg<DP, SM, 4, 1, 32>(p, st);
+  else return fwd_cfg<DP, SM, 4, 1, 64>(p, st);
+}
+
+template <int DP, bool SM>
+hipError_t dq_default(const Params& p, hipStream_t st) {
+  if constexpr (kIsF32) return dq_cfg<DP, SM, 4, 1, 32>(p, st);
+  else if constexpr (DP <= 64) return dq_cfg<DP, SM, 4, 1, 64>(p, st);
+  else return dq_cfg<DP, SM, 4, 1, 32>(p, st);
+}
+
+template <int DP, bool SM>
+hipError_t dkdv_default(const Params& p, hipStream_t st) {
+  if constexpr (kIsF32) return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
+  else if constexpr (DP <= 64) return dkdv_cfg<DP, SM, 4, 1, 64>(p, st);
+  else return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
+}
+
+// ---- tuning candidates (bf16, 32 < D <= 64) ------------------------------
+template <int DP, bool SM>
+hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
+#if RBF_ELEM_ID == 0
+  if constexpr (DP <= 64) {
+  static const int choice = env_choice("RBF_ATTN_FWD_CFG");
+  switch (choice) {
+    case 0: return fwd_cfg<DP, SM, 4, 1, 64>(p, st);
+    case 1: return fwd_cfg<DP, SM, 2, 2, 64>(p, st);
+    case 2: return fwd_cfg<DP, SM, 4, 2, 64>(p, st);
+    case 3: return fwd_cfg<DP, SM, 2, 1, 64>(p, st);
+    case 4: return fwd_cfg<DP, SM, 4, 1, 128>(p, st);
+    case 5: return fwd_cfg<DP, SM, 8, 1, 64>(p, st);
+    default: break;
+  }
+  }
+#endif
+  return fwd_default<DP, SM>(p, st);
+}
+
+template <int DP, bool SM>
+hipError_t dq_any_cfg(const Params& p, hipStream_t st) {
+#if RBF_ELEM_ID == 0
+  if constexpr (DP <= 64) {
+  static const int choice = env_choice("RBF_ATTN_DQ_CFG");
+  switch (choice) {
+    case 0: return dq_cfg<DP, SM, 4, 1, 64>(p, st);
+    case 1: return dq_cfg<DP, SM, 2, 2, 64>(p, st);
+    case 2: return dq_cfg<DP, SM, 4, 2, 64>(p, st);
+    case 3: return dq_cfg<DP, SM, 4, 2, 32>(p, st);
+    case 4: return dq_cfg<DP, SM, 4, 1, 32>(p, st);
+    case 5: return dq_cfg<DP, SM, 8, 1, 64>(p, st);
+    default: break;
+  }
+  }
+#endif
+  return dq_default<DP, SM>(p, st);
+}
+
+template <int DP, bool SM>
+hipError_t dkdv_any_cfg(const Params& p, hipStream_t st) {
+#if RBF_ELEM_ID == 0
+  if constexpr (DP <= 64) {
+  static const int choice = env_choice("RBF_ATTN_DKDV_CFG");
+  switch (choice) {
+    case 0: return dkdv_cfg<DP, SM, 4, 1, 64>(p, st);
+    case 1: return dkdv_cfg<DP, SM, 2, 2, 64>(p, st);
+    case 2: return dkdv_cfg<DP, SM, 4, 2, 64>(p, st);
+    case 3: return dkdv_cfg<DP, SM, 4, 2, 32>(p, st);
+    case 4: return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
+    case 5: return dkdv_cfg<DP, SM, 8, 1, 64>(p, st);
+    default: break;
+  }
+  }
+#endif
+  return dkdv_default<DP, SM>(p, st);
+}
+
 // Head dim D (a multiple of 8 in [8, 128]) runs on the kernel for the next
-// padded width DP in {32, 64, 128}; features D..DP-1 are zero-filled.
-#define RBF_DISPATCH(FN)                                               \
-  do {                                                                 \
-    const bool sm = (variant == 0);                                    \
-    if (p.D <= 32) return sm ? FN<32, true>(p, st) : FN<32, false>(p, st); \
-    if (p.D <= 64) return sm ? FN<64, true>(p, st) : FN<64, false>(p, st); \
-    return sm ? FN<128, true>(p, st) : FN<128, false>(p, st);          \
+// padded width DP in {32, 64, 128}; features D..DP-1 are zero-filled.  Only
+// the softmax bf16 path with D in (32, 64] carries tuning candidates.
+#define RBF_DISPATCH(DEF, ANY)                                                      \
+  do {                                                                              \
+    const bool sm = (variant == 0);                                                 \
+    if (p.D <= 32) return sm ? DEF<32, true>(p, st) : DEF<32, false>(p, st);        \
+    if (p.D <= 64) return sm ? ANY<64, true>(p, st) : DEF<64, false>(p, st);        \
+    return sm ? ANY<128, true>(p, st) : DEF<128, false>(p, st);                     \
   } while (0)
 
-hipError_t fwd_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(fwd); }
-hipError_t dq_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(dq); }
-hipError_t dkdv_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(dkdv); }
+hipError_t fwd_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(fwd_default, fwd_any_cfg); }
+hipError_t dq_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(dq_default, dq_any_cfg); }
+hipError_t dkdv_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(dkdv_default, dkdv_any_cfg); }
 
 #undef RBF_DISPATCH
 
