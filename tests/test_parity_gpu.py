@@ -249,3 +249,21 @@ def test_empty_batch(cuda_device):
     q = torch.zeros(0, 2, 16, 64, device=cuda_device, dtype=torch.bfloat16)
     out = ra.run_triton_rbf(q, q, q)
     assert out.shape == q.shape
+
+
+# ---------------------------------------------------------------------------
+# Committed fixtures (tests/golden/c1_slices.npz): fp32, compared directly.
+# ---------------------------------------------------------------------------
+def test_golden_fixture_fp32(cuda_device):
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "c1_slices.npz")
+    gold = np.load(path)
+    g = float(gold["gamma"])
+    q, k, v, do = (torch.from_numpy(gold[n]).to(cuda_device) for n in ("q", "k", "v", "do"))
+    outs = run_ours(q, k, v, do, True, True, g, 0)
+    for name, got in zip(("O", "dq", "dk", "dv"), outs):
+        check(f"golden softmax {name}", got, gold[f"softmax_{name}"].astype(np.float64), torch.float32)
+    _, L = torch.ops.rbf_attn_amd.scaled_fwd_ex(q, k, v, True, g, 0)
+    check("golden softmax L", L, gold["softmax_L"].astype(np.float64), torch.float32)
+    outs = run_ours(0.5 * q, 0.5 * k, 0.5 * v, 0.5 * do, False, True, g, 0)
+    for name, got in zip(("O", "dq", "dk", "dv"), outs):
+        check(f"golden non-softmax {name}", got, gold[f"nonsoftmax_{name}"].astype(np.float64), torch.float32)
