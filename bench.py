@@ -102,6 +102,60 @@ def measured_traffic(workload: str, kernel: str):
         return None
 
 
+def train_step_bench(dev, steps: int, warmup: int):
+    """one next-token training step (bf16 autocast fwd,
+    bwd, AdamW) of the 8-layer d512 RBF transformer on synthetic tokens,
+    with the HIP attention kernels.  Returns a dict for the JSON line."""
+    import torch
+
+    from rbf_attention_amd import model as M
+
+    cfg = M.ModelConfig()
+    batch, seq = 32, 512
+    torch.manual_seed(0)
+    model = M.CausalLM(cfg).to(dev)
+    tr = M.Trainer(model)
+    tokens = M.synthetic_tokens(batch, seq, cfg.vocab_size, device=dev)
+    first = tr.step(tokens)
+    for _ in range(max(0, warmup - 1)):
+        tr.step(tokens)
+    stream = torch.cuda.current_stream(dev)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        last = tr.step(tokens)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {
+        "metric": "train-step tokens/s",
+        "value": round(batch * seq / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "ms_per_step": round(ms, 4),
+        "steps": steps,
+        "warmup": warmup,
+        "dtype": "bf16 autocast",
+        "loss_first": round(float(first), 4),
+        "loss_last": round(float(last), 4),
+        "attention_tflop_per_step": round(M.attention_flops_per_step(cfg, batch, seq) / 1e12, 4),
+        "config": {
+            "workload": "c5_train_step",
+            "layers": cfg.num_layers,
+            "d_model": cfg.d_model,
+            "heads": cfg.num_heads,
+            "registers": cfg.num_registers,
+            "vocab": cfg.vocab_size,
+            "tied_embeddings": cfg.tie_embeddings,
+            "batch": batch,
+            "seq_len": seq,
+            "optimizer": "AdamW",
+            "params": M.gpt_param_count(model),
+        },
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -110,6 +164,8 @@ def main() -> int:
     ap.add_argument("--workload", default="c2_model_bf16")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-train-step", action="store_true", help="skip the config-5 train-step measurement")
+    ap.add_argument("--train-steps", type=int, default=20)
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="run one device copy of this many MiB before timing (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -230,6 +286,10 @@ def main() -> int:
             "traffic": measured_traffic(w.name, dom),
         },
     }
+    if not args.no_train_step:
+        log("train step (config 5) ...")
+        result["train_step"] = train_step_bench(dev, args.train_steps, 3)
+        log(f"  {result['train_step']['value']} tokens/s, {result['train_step']['ms_per_step']} ms/step")
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)

@@ -33,7 +33,7 @@ def non_softmax_math_forward(q, k, v, gamma: float, is_causal: bool = True, chun
     qf = q.float().reshape(B * H, N, D)
     kf = k.float().reshape(B * H, N, D)
     vf = v.float().reshape(B * H, N, D)
-    mask = torch.ones(N, N, dtype=torch.bool).triu_(1) if is_causal else None
+    mask = torch.ones(N, N, dtype=torch.bool, device=q.device).triu_(1) if is_causal else None
     outs = []
     for s in range(0, B * H, chunk):
         qs, ks, vs = qf[s : s + chunk], kf[s : s + chunk], vf[s : s + chunk]

@@ -1,0 +1,229 @@
+"""Caller layer of the RBF attention op: attention module, transformer block
+and causal LM, counterparts of the reference's model code for the RBF
+attention types, and the config-5 training step.
+
+* ``RBFAttention``  <- ``CustomCausalAttention`` (rbf_attention.py:1608-1762) for
+  ``attention_type`` "rbf_triton" (1736-1737) and "rbf_non_softmax" (1754-1755):
+  packed qkv projection, SuSiE unrotated sinusoidal position embeddings with a
+  learnable per-head ``pos_weight`` (1644-1688, utility at 1540-1544), learned
+  register position embeddings (1647-1650, 1672-1682), optional XSA (1757-1759),
+  output projection.
+* ``TransformerBlock`` <- train_rbf_transformer.py:113-151 (pre-LayerNorm, MLP
+  4x with GELU).
+* ``CausalLM`` <- train_rbf_transformer.py:154-244 (token embedding, zero-initialised
+  register tokens prepended and sliced off, final LayerNorm, logits), plus an
+  option to tie the output projection to the token embedding.
+
+Attention always runs on the HIP kernels through the ``rbf_attn_v5`` /
+``rbf_attn_amd`` ops; there is no fallback.
+"""
+from __future__ import annotations
+
+import dataclasses
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+
+
+def unrotated_sinusoids(seq_len: int, dim: int, device=None, theta: float = 10000.0) -> torch.Tensor:
+    """[sin(t f), cos(t f)] with f_i = theta^(-2i/dim): the SuSiE table
+    (rbf_attention.py:1540-1544)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, dim, 2, device=device).float() / dim))
+    t = torch.arange(seq_len, device=device).float()
+    freqs = torch.outer(t, inv_freq)
+    return torch.cat((freqs.sin(), freqs.cos()), dim=-1)
+
+
+class RBFAttention(nn.Module):
+    ATTENTION_TYPES = ("rbf", "rbf_non_softmax")
+
+    def __init__(
+        self,
+        num_heads: int,
+        emb_dims: int,
+        max_seq_len: int = 2048,
+        attention_type: str = "rbf",
+        use_susie: bool = True,
+        num_registers: int = 0,
+        pos_weight_init: float = 0.5,
+        sm_scale: float | None = None,
+        registers_visible_to_all: bool = False,
+        apply_xsa: bool = False,
+    ):
+        super().__init__()
+        if attention_type not in self.ATTENTION_TYPES:
+            raise ValueError(f"attention_type must be one of {self.ATTENTION_TYPES}, got {attention_type!r}")
+        if emb_dims % num_heads:
+            raise ValueError("emb_dims must be divisible by num_heads")
+        self.num_heads = num_heads
+        self.head_dim = emb_dims // num_heads
+        self.attention_type = attention_type
+        self.num_registers = num_registers
+        self.sm_scale = sm_scale
+        self.num_prefix = num_registers if registers_visible_to_all else 0
+        self.apply_xsa = apply_xsa
+        self.qkv_proj = nn.Linear(emb_dims, 3 * emb_dims)
+        self.proj = nn.Linear(emb_dims, emb_dims)
+        self.use_susie = use_susie
+        if use_susie:
+            self.pos_weight = nn.Parameter(torch.full((1, num_heads, 1, self.head_dim // 2), float(pos_weight_init)))
+            if num_registers > 0:
+                self.reg_pos_emb = nn.Parameter(torch.randn(1, num_heads, num_registers, self.head_dim) * 0.02)
+            self.register_buffer("susie_cache", unrotated_sinusoids(max_seq_len, self.head_dim), persistent=False)
+
+    def position_embedding(self, s: int, dtype: torch.dtype) -> torch.Tensor:
+        """(1, H, s, head_dim) SuSiE embedding added to q and k."""
+        weight = torch.cat([self.pos_weight, self.pos_weight], dim=-1).to(dtype)
+        text_len = s - self.num_registers if self.num_registers > 0 else s
+        pos = self.susie_cache[:text_len].view(1, 1, text_len, self.head_dim).to(dtype) * weight
+        if self.num_registers > 0:
+            pos = torch.cat([self.reg_pos_emb.to(dtype), pos], dim=2)
+        return pos
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        b, s, _ = x.shape
+        qkv = self.qkv_proj(x)
+        # "b s (qkv h n) -> qkv b h s n" as strided views (rbf_attention.py:1660-1662)
+        q, k, v = qkv.view(b, s, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4)
+        if self.use_susie:
+            pos = self.position_embedding(s, q.dtype)
+            q, k = q + pos, k + pos
+        fn = ops.run_triton_rbf if self.attention_type == "rbf" else ops.run_triton_non_softmax_rbf
+        out = fn(q, k, v, True, sm_scale=self.sm_scale, num_prefix=self.num_prefix)
+        if self.apply_xsa:
+            v_n = F.normalize(v, dim=-1)
+            out = out - (out * v_n).sum(dim=-1, keepdim=True) * v_n
+        out = out.transpose(1, 2).reshape(b, s, self.num_heads * self.head_dim)
+        return self.proj(out)
+
+
+class TransformerBlock(nn.Module):
+    def __init__(self, emb_dim: int, num_heads: int, max_seq_len: int, **attn_kw):
+        super().__init__()
+        self.attn = RBFAttention(num_heads, emb_dim, max_seq_len, **attn_kw)
+        self.ln1 = nn.LayerNorm(emb_dim)
+        self.ff = nn.Sequential(nn.Linear(emb_dim, emb_dim * 4), nn.GELU(), nn.Linear(emb_dim * 4, emb_dim))
+        self.ln2 = nn.LayerNorm(emb_dim)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x = x + self.attn(self.ln1(x))
+        return x + self.ff(self.ln2(x))
+
+
+@dataclasses.dataclass
+class ModelConfig:
+    """Defaults are BASELINE config 5; the reference's defaults are
+    d_model=256, 4 layers, 4 heads, 1 register, pos_weight 0.5, untied logits
+    (train_rbf_transformer.py:18-28, rbf_attention.py:1644-1646)."""
+
+    vocab_size: int = 8192
+    d_model: int = 512
+    num_layers: int = 8
+    num_heads: int = 8
+    max_seq_len: int = 1024
+    num_registers: int = 4
+    attention_type: str = "rbf"
+    pos_weight_init: float = 1.0
+    tie_embeddings: bool = True
+    sm_scale: float | None = None
+    registers_visible_to_all: bool = False
+
+
+class CausalLM(nn.Module):
+    def __init__(self, cfg: ModelConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.num_registers = cfg.num_registers
+        if cfg.num_registers > 0:
+            # zero registers: initial distance to a query is just ||q||^2
+            # (train_rbf_transformer.py:176-180)
+            self.register_tokens = nn.Parameter(torch.zeros(cfg.num_registers, cfg.d_model))
+        self.token_emb = nn.Embedding(cfg.vocab_size, cfg.d_model)
+        if cfg.tie_embeddings:
+            # The table doubles as the output projection: N(0, 1) rows (the
+            # nn.Embedding default, fine for the reference's untied head) would
+            # give logits of std ~sqrt(d_model) at initialisation.
+            nn.init.normal_(self.token_emb.weight, std=cfg.d_model ** -0.5)
+        self.blocks = nn.ModuleList(
+            TransformerBlock(
+                cfg.d_model,
+                cfg.num_heads,
+                cfg.max_seq_len + cfg.num_registers,
+                attention_type=cfg.attention_type,
+                num_registers=cfg.num_registers,
+                pos_weight_init=cfg.pos_weight_init,
+                sm_scale=cfg.sm_scale,
+                registers_visible_to_all=cfg.registers_visible_to_all,
+            )
+            for _ in range(cfg.num_layers)
+        )
+        self.ln_f = nn.LayerNorm(cfg.d_model)
+        self.to_logits = None if cfg.tie_embeddings else nn.Linear(cfg.d_model, cfg.vocab_size)
+
+    def forward(self, idx: torch.Tensor) -> torch.Tensor:
+        B, T = idx.shape
+        x = self.token_emb(idx)
+        if self.num_registers > 0:
+            x = torch.cat([self.register_tokens.unsqueeze(0).expand(B, -1, -1).to(x.dtype), x], dim=1)
+        for blk in self.blocks:
+            x = blk(x)
+        if self.num_registers > 0:
+            x = x[:, self.num_registers:, :]
+        x = self.ln_f(x)
+        if self.to_logits is None:
+            return F.linear(x, self.token_emb.weight)
+        return self.to_logits(x)
+
+
+def attention_flops_per_step(cfg: ModelConfig, batch: int, seq: int) -> float:
+    """Algorithmic attention fwd+bwd flops of one training step (14 D per
+    visible causal pair per head and layer, registers included)."""
+    n = seq + cfg.num_registers
+    d = cfg.d_model // cfg.num_heads
+    return 14.0 * d * n * (n + 1) / 2 * batch * cfg.num_heads * cfg.num_layers
+
+
+class Trainer:
+    """One next-token training step: bf16 autocast forward, fp32 cross
+    entropy, backward, AdamW (the reference's loop, train_rbf_transformer.py:
+    319-349, without the fp16 GradScaler that bf16 does not need)."""
+
+    def __init__(self, model: CausalLM, lr: float = 1e-3, weight_decay: float = 0.01):
+        self.model = model
+        self.opt = torch.optim.AdamW(model.parameters(), lr=lr, weight_decay=weight_decay)
+
+    def step(self, tokens: torch.Tensor) -> torch.Tensor:
+        """tokens: (B, T+1) int64; trains on x = tokens[:, :-1], y = tokens[:, 1:]."""
+        x, y = tokens[:, :-1], tokens[:, 1:]
+        self.opt.zero_grad(set_to_none=True)
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            logits = self.model(x)
+        loss = F.cross_entropy(logits.float().reshape(-1, logits.shape[-1]), y.reshape(-1))
+        loss.backward()
+        self.opt.step()
+        return loss.detach()
+
+
+def synthetic_tokens(batch: int, seq: int, vocab: int, seed: int = 42, device=None) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, vocab, (batch, seq + 1), generator=g).to(device)
+
+
+def gpt_param_count(model: nn.Module) -> int:
+    return sum(p.numel() for p in model.parameters())
+
+
+__all__ = [
+    "RBFAttention",
+    "TransformerBlock",
+    "CausalLM",
+    "ModelConfig",
+    "Trainer",
+    "synthetic_tokens",
+    "attention_flops_per_step",
+    "unrotated_sinusoids",
+    "gpt_param_count",
+]
