@@ -33,6 +33,9 @@ COMMON_FLAGS = [
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    # NaN never reaches a max/compare on a path whose result is used (masked
+    # logits are -inf, never NaN), so fmaxf needs no NaN canonicalisation.
+    "-fno-honor-nans",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
     "-Wno-unused-command-line-argument",

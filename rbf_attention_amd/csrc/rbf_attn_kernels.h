@@ -33,6 +33,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace rbf {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -158,6 +160,28 @@ __device__ inline int swap23(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 
 // Row of accumulator element i held by lane half h (32x32 MFMA C layout).
 __device__ inline int crow(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
 
+// Transposed operand fragment from a ROW-major 16-bit LDS tile X[token][feature]
+// with row stride LD elements (gfx950 ds_read_b64_tr_b16, two reads): lane
+// (m = lane % 32, h = lane / 32) receives feature fbase + m of the 8 tokens
+// tbase + 8(s/4) + 4h + s%4, s = 0..7 -- the contraction order of a P / dS
+// accumulator reused as the other operand (crow(8t + s, h) with tbase = 16t).
+// Within each 16-lane group, lane g addresses token row R0 + g/4 at feature
+// column n0 + 4(g%4) and receives X[R0 + e][n0 + g] for e = 0..3.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+template <typename T, int LD>
+__device__ inline typename Elem<T>::frag ld_tr8(const T* tile, int tbase, int fbase, int lane) {
+  static_assert(sizeof(T) == 2, "transposing LDS reads are for 16-bit elements");
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+  const int g = lane & 15;
+  const int row = tbase + 4 * (lane >> 5) + (g >> 2);
+  const int col = fbase + 16 * ((lane >> 4) & 1) + 4 * (g & 3);
+  const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + row * LD + col));
+  const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + (row + 8) * LD + col));
+  typedef short s16x8_t __attribute__((ext_vector_type(8)));
+  const s16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(typename Elem<T>::frag, v);
+}
+
 // Offset of the 8-token chunk starting at tile-local token position p8
 // (a multiple of 8) in feature row `feat` of a transposed tile with ROWS
 // tokens (see Tile::store_trans).
@@ -214,23 +238,32 @@ __device__ inline f32x16_t zero16() {
   return z;
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// sum_e a[e] * b[e] over 8 elements in fp32 (v_dot2_f32_{bf16,f16} for the
+// 16-bit types: products exact, fp32 accumulation).
 template <typename T>
-__device__ inline float sumsq8(typename Elem<T>::frag f) {
+__device__ inline float dot8(typename Elem<T>::frag a, typename Elem<T>::frag b) {
   float s = 0.f;
+  if constexpr (sizeof(T) == 2) {
+    typedef typename std::conditional<std::is_same<T, __bf16>::value, bf16x2_t, f16x2_t>::type pair;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float x = (float)f[e];
-    s = fmaf(x, x, s);
+    for (int e = 0; e < 8; e += 2) {
+      const pair x = {a[e], a[e + 1]}, y = {b[e], b[e + 1]};
+      if constexpr (std::is_same<T, __bf16>::value) s = __builtin_amdgcn_fdot2_f32_bf16(x, y, s, false);
+      else s = __builtin_amdgcn_fdot2(x, y, s, false);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s = fmaf((float)a[e], (float)b[e], s);
   }
   return s;
 }
 
 template <typename T>
-__device__ inline float dot8(typename Elem<T>::frag a, typename Elem<T>::frag b) {
-  float s = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) s = fmaf((float)a[e], (float)b[e], s);
-  return s;
+__device__ inline float sumsq8(typename Elem<T>::frag f) {
+  return dot8<T>(f, f);
 }
 
 template <typename T>
@@ -252,8 +285,11 @@ struct Tile {
   static constexpr int PER = (UNITS + NT - 1) / NT;
   static_assert(NT % CPR == 0, "a row pair must not straddle threads unevenly");
   frag r[PER][2];
+  int tok0_, n_;  // token of row 0 and sequence length of the loaded tile
 
   __device__ inline void load(const T* base, int64_t sn, int tok0, int N, int D, int tid) {
+    tok0_ = tok0;
+    n_ = N;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int u = tid + j * NT;
@@ -297,10 +333,13 @@ struct Tile {
       // every feature row 8dc + c shares the swizzle value dc
       const int spos = (((pos >> 3) ^ (dc & (ROWS / 8 - 1))) << 3) | (pos & 7);
       if constexpr (sizeof(T) == 2) {
+        const u32x4_t a = __builtin_bit_cast(u32x4_t, r[j][0]);  // row 2rp: elements (2m, 2m+1) in dword m
+        const u32x4_t b = __builtin_bit_cast(u32x4_t, r[j][1]);  // row 2rp+1
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const uint32_t w = bits16<T>(r[j][0][c]) | (bits16<T>(r[j][1][c]) << 16);
-          *reinterpret_cast<uint32_t*>(lds + (dc * 8 + c) * LDT + spos) = w;
+        for (int m = 0; m < 4; ++m) {
+          // (row0[2m], row1[2m]) and (row0[2m+1], row1[2m+1]) as 16-bit pairs
+          *reinterpret_cast<uint32_t*>(lds + (dc * 8 + 2 * m) * LDT + spos) = __builtin_amdgcn_perm(b[m], a[m], 0x05040100u);
+          *reinterpret_cast<uint32_t*>(lds + (dc * 8 + 2 * m + 1) * LDT + spos) = __builtin_amdgcn_perm(b[m], a[m], 0x07060302u);
         }
       } else {
 #pragma unroll
@@ -312,8 +351,11 @@ struct Tile {
     }
   }
 
-  // nrm[row] = sign * 0.5 * ||row||^2 in fp32 (from the input-dtype values).
-  __device__ inline void store_halfnorm(float* nrm, int tid, float sign) const {
+  // nrm[row] = -0.5 * ||row||^2 in fp32 (from the input-dtype values), and
+  // -inf for padding rows (tokens outside [0, N)): used as the initial value
+  // of an S accumulator, it makes every logit against a padding key -inf, so
+  // padding needs no element mask.
+  __device__ inline void store_neg_halfnorm(float* nrm, int tid) const {
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int u = tid + j * NT;
@@ -321,7 +363,8 @@ struct Tile {
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const float s = group_sum<CPR>(sumsq8<T>(r[j][e]));
-        if (dc == 0 && u < UNITS) nrm[2 * rp + e] = (0.5f * sign) * s;
+        const int tok = tok0_ + 2 * rp + e;
+        if (dc == 0 && u < UNITS) nrm[2 * rp + e] = (tok >= 0 && tok < n_) ? -0.5f * s : -__builtin_inff();
       }
     }
   }
@@ -350,8 +393,48 @@ __device__ inline bool blk_any(int q0, int k0, bool causal, int npre) {
 __device__ inline bool blk_full(int q0, int k0, bool causal, int npre) {
   return q0 >= 0 && k0 >= 0 && (!causal || k0 + 31 <= q0 || k0 + 31 < npre);
 }
+// Like blk_full, but padding tokens (block 0 when N % 32 != 0) count as
+// visible: their logits are already -inf through the accumulator's initial
+// value (padding keys, and padding queries in the dK/dV kernel) or their rows
+// are never stored (padding queries in the forward and dQ kernels).
+__device__ inline bool blk_nomask(int q0, int k0, bool causal, int npre) {
+  return !causal || k0 + 31 <= q0 || k0 + 31 < npre;
+}
 __device__ inline bool elem_vis(int i, int j, bool causal, int npre) {
   return i >= 0 && j >= 0 && (!causal || j <= i || j < npre);
+}
+
+// Row offset of accumulator element i without the lane-half term:
+// crow(i, h) = crow0(i) + 4h.
+__device__ inline constexpr int crow0(int i) { return 8 * (i >> 2) + (i & 3); }
+
+// The keys visible to query i form one range [0, last_key(i)]: j <= i, or a
+// prefix (register) key j < npre, or every key when not causal.
+__device__ inline int last_key(int i, int N, bool causal, int npre) {
+  if (i < 0) return -1;
+  return causal ? max(i, npre - 1) : N - 1;
+}
+// The queries that see key j form one range [first_query(j), N).
+__device__ inline int first_query(int j, bool causal, int npre) {
+  if (j < 0) return 1 << 30;
+  return (!causal || j < npre) ? 0 : j;
+}
+
+// Keys along the accumulator rows (fwd, dQ: lane = query): element i holds key
+// k0 + crow(i, h); keep it iff 0 <= key <= jmax.
+__device__ inline void mask_key_rows(f32x16_t& s, int k0, int h, int jmax) {
+  const int lo = -k0 - 4 * h, hi = jmax - k0 - 4 * h;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (crow0(i) < lo || crow0(i) > hi) s[i] = -__builtin_inff();
+}
+// Queries along the accumulator rows (dK/dV: lane = key): element i holds
+// query q0 + crow(i, h); keep it iff query >= ilo (queries never exceed N-1).
+__device__ inline void mask_query_rows(f32x16_t& s, int q0, int h, int ilo) {
+  const int lo = ilo - q0 - 4 * h;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (crow0(i) < lo) s[i] = -__builtin_inff();
 }
 
 // Per-slot values of a 32-entry fp32 LDS vector for the C layout rows of lane
@@ -383,14 +466,18 @@ __device__ inline f32x16_t splat16(float x) {
 //   P   = exp2(c S^T - m) with a lazily raised running max m,
 //   O^T += V^T P^T.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX>
+template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX, bool EARLY = true, int PF = 1>
 __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
+  static_assert(PF == 1 || PF == 2, "prefetch depth is 1 or 2 tiles");
   typedef Elem<T> E;
   typedef typename E::frag frag;
   constexpr int NT = 64 * W, KB = BN / 32, KS = DP / 16, ND = DP / 32, GB = W * QPW;
   constexpr int LDR = DP + E::PAD, LDT = BN + E::PAD;
+  // 16-bit types keep V row-major and read V^T with transposing LDS reads;
+  // fp32 stages a transposed copy.
+  constexpr bool TR = sizeof(T) == 2;
   __shared__ __attribute__((aligned(16))) T sK[2][BN * LDR];
-  __shared__ __attribute__((aligned(16))) T sVt[2][DP * LDT];
+  __shared__ __attribute__((aligned(16))) T sVt[2][TR ? BN * LDR : DP * LDT];
   __shared__ __attribute__((aligned(16))) float sKn[2][BN];
 
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
@@ -419,13 +506,14 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   const int last_blk = (hi - 1 - org) >> 5;
   const int nkt = (last_blk + kshift) / KB + 1;
 
-  int q0[QPW], qtok[QPW];
+  int q0[QPW], qtok[QPW], jmax[QPW];
   frag qf[QPW][KS];
   float qoff[QPW];
 #pragma unroll
   for (int j = 0; j < QPW; ++j) {
     q0[j] = org + 32 * (qblk0 + j);
     qtok[j] = q0[j] + n;
+    jmax[j] = last_key(qtok[j], N, causal, npre);
     const bool ok = wave_on && qtok[j] >= 0;
 #pragma unroll
     for (int t = 0; t < KS; ++t)
@@ -450,24 +538,24 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
     l_run[j] = 0.f;
   }
 
-  Tile<T, BN, DP, NT> tk, tv;
-  {
-    const int tok0 = org + 32 * (-kshift);
+  // Key tiles are staged global -> registers -> LDS.  With PF = 2 two
+  // register sets alternate, so the global loads of tile kt+2 are in flight
+  // while tile kt is computed and tile kt+1 waits in registers.
+  typedef Tile<T, BN, DP, NT> TileT;
+  auto load_kv = [&](int kt, TileT& tk, TileT& tv) {
+    const int tok0 = org + 32 * (kt * KB - kshift);
     tk.load(K, p.sk[2], tok0, N, D, tid);
     tv.load(V, p.sv[2], tok0, N, D, tid);
-  }
-  for (int kt = 0; kt < nkt; ++kt) {
+  };
+  auto tile_step = [&](int kt, TileT& tk, TileT& tv) {
     const int buf = kt & 1;
     tk.template store_rows<LDR>(sK[buf], tid);
-    tk.store_halfnorm(sKn[buf], tid, -1.f);
-    tv.template store_trans<LDT>(sVt[buf], tid);
+    tk.store_neg_halfnorm(sKn[buf], tid);
+    if constexpr (TR) tv.template store_rows<LDR>(sVt[buf], tid);
+    else tv.template store_trans<LDT>(sVt[buf], tid);
     __syncthreads();
-    if (kt + 1 < nkt) {
-      const int tok1 = org + 32 * ((kt + 1) * KB - kshift);
-      tk.load(K, p.sk[2], tok1, N, D, tid);
-      tv.load(V, p.sv[2], tok1, N, D, tid);
-    }
-    if (!wave_on) continue;
+    if (kt + PF < nkt) load_kv(kt + PF, tk, tv);
+    if (!wave_on) return;
     const int kblk0 = kt * KB - kshift;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
@@ -484,18 +572,33 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
 #pragma unroll
       for (int t = 0; t < KS; ++t) kA[t] = ld8<T>(sK[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h);
       const f32x16_t kinit = ld_rows16(sKn[buf] + 32 * kb, h);
+      f32x16_t sacc[QPW];
+#pragma unroll
+      for (int j = 0; j < QPW; ++j) {
+        if (!act[j]) continue;
+        sacc[j] = kinit;
+#pragma unroll
+        for (int t = 0; t < KS; ++t) sacc[j] = E::mma(kA[t], qf[j][t], sacc[j]);
+      }
+      // V^T fragments are read while the S MFMAs and the softmax run (EARLY),
+      // or next to the P.V MFMAs.
+      frag vA[ND][2];
+      auto read_v = [&]() {
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            if constexpr (TR) vA[d][t] = ld_tr8<T, LDR>(sVt[buf], 32 * kb + 16 * t, 32 * d, lane);
+            else vA[d][t] = ld8<T>(sVt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h));
+          }
+      };
+      if constexpr (EARLY) read_v();
       frag pf[QPW][2];
 #pragma unroll
       for (int j = 0; j < QPW; ++j) {
         if (!act[j]) continue;
-        f32x16_t s = kinit;
-#pragma unroll
-        for (int t = 0; t < KS; ++t) s = E::mma(kA[t], qf[j][t], s);
-        if (!blk_full(q0[j], k0, causal, npre)) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            if (!elem_vis(qtok[j], k0 + crow(i, h), causal, npre)) s[i] = -__builtin_inff();
-        }
+        f32x16_t s = sacc[j];
+        if (!blk_nomask(q0[j], k0, causal, npre)) mask_key_rows(s, k0, h, jmax[j]);
         float moff;
         if constexpr (SOFTMAX) {
           const float mx = xhalf_max(tree_max16(s));
@@ -520,15 +623,26 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
         }
         if constexpr (SOFTMAX) l_run[j] += tree_sum16(pv);
       }
+      if constexpr (!EARLY) read_v();
 #pragma unroll
       for (int d = 0; d < ND; ++d)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const frag vA = ld8<T>(sVt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h));
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int j = 0; j < QPW; ++j)
-            if (act[j]) oacc[j][d] = E::mma(vA, pf[j][t], oacc[j][d]);
-        }
+            if (act[j]) oacc[j][d] = E::mma(vA[d][t], pf[j][t], oacc[j][d]);
+    }
+  };
+  TileT tkA, tvA;
+  load_kv(0, tkA, tvA);
+  if constexpr (PF == 1) {
+    for (int kt = 0; kt < nkt; ++kt) tile_step(kt, tkA, tvA);
+  } else {
+    TileT tkB, tvB;
+    if (nkt > 1) load_kv(1, tkB, tvB);
+    for (int kt = 0; kt < nkt; kt += 2) {
+      tile_step(kt, tkA, tvA);
+      if (kt + 1 < nkt) tile_step(kt + 1, tkB, tvB);
     }
   }
 
@@ -565,14 +679,17 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
 //   S^T = K Q^T (init -0.5||k||^2), P = exp2(c S^T - L),
 //   dP^T = V dO^T (init -Delta), dS = P dP^T, dQ^T += K^T dS^T.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX>
+template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX, bool EARLY = true>
 __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   constexpr int NT = 64 * W, KB = BN / 32, KS = DP / 16, ND = DP / 32, GB = W * QPW;
   constexpr int LDR = DP + E::PAD, LDT = BN + E::PAD;
+  // 16-bit types read K^T from the row-major K tile with transposing LDS
+  // reads; fp32 stages a transposed copy.
+  constexpr bool TR = sizeof(T) == 2;
   __shared__ __attribute__((aligned(16))) T sK[2][BN * LDR];
-  __shared__ __attribute__((aligned(16))) T sKt[2][DP * LDT];
+  __shared__ __attribute__((aligned(16))) T sKt[TR ? 1 : 2][TR ? 8 : DP * LDT];
   __shared__ __attribute__((aligned(16))) T sV[2][BN * LDR];
   __shared__ __attribute__((aligned(16))) float sKn[2][BN];
 
@@ -604,7 +721,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   const int last_blk = (hi - 1 - org) >> 5;
   const int nkt = (last_blk + kshift) / KB + 1;
 
-  int q0[QPW], qtok[QPW];
+  int q0[QPW], qtok[QPW], jmax[QPW];
   frag qf[QPW][KS], df[QPW][KS];
   float off[QPW];
   f32x16_t ndel[QPW];  // -Delta broadcast: the dP accumulator's initial value
@@ -612,6 +729,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   for (int j = 0; j < QPW; ++j) {
     q0[j] = org + 32 * (qblk0 + j);
     qtok[j] = q0[j] + n;
+    jmax[j] = last_key(qtok[j], N, causal, npre);
     const bool qvalid = wave_on && qtok[j] >= 0;
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
@@ -661,8 +779,8 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   for (int kt = 0; kt < nkt; ++kt) {
     const int buf = kt & 1;
     tk.template store_rows<LDR>(sK[buf], tid);
-    tk.template store_trans<LDT>(sKt[buf], tid);
-    tk.store_halfnorm(sKn[buf], tid, -1.f);
+    if constexpr (!TR) tk.template store_trans<LDT>(sKt[buf], tid);
+    tk.store_neg_halfnorm(sKn[buf], tid);
     tv.template store_rows<LDR>(sV[buf], tid);
     __syncthreads();
     if (kt + 1 < nkt) {
@@ -690,21 +808,38 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
         vA[t] = ld8<T>(sV[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h);
       }
       const f32x16_t kinit = ld_rows16(sKn[buf] + 32 * kb, h);
+      f32x16_t sacc[QPW], dpacc[QPW];
+#pragma unroll
+      for (int j = 0; j < QPW; ++j) {
+        if (!act[j]) continue;
+        sacc[j] = kinit;
+        dpacc[j] = ndel[j];
+#pragma unroll
+        for (int t = 0; t < KS; ++t) {
+          sacc[j] = E::mma(kA[t], qf[j][t], sacc[j]);
+          dpacc[j] = E::mma(vA[t], df[j][t], dpacc[j]);
+        }
+      }
+      // K^T fragments are read while the S / dP MFMAs and the softmax run
+      // (EARLY), or next to the dQ MFMAs.
+      frag ktA[ND][2];
+      auto read_kt = [&]() {
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            if constexpr (TR) ktA[d][t] = ld_tr8<T, LDR>(sK[buf], 32 * kb + 16 * t, 32 * d, lane);
+            else ktA[d][t] = ld8<T>(sKt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h));
+          }
+      };
+      if constexpr (EARLY) read_kt();
       frag sf[QPW][2];
 #pragma unroll
       for (int j = 0; j < QPW; ++j) {
         if (!act[j]) continue;
-        f32x16_t s = kinit, dp = ndel[j];
-#pragma unroll
-        for (int t = 0; t < KS; ++t) {
-          s = E::mma(kA[t], qf[j][t], s);
-          dp = E::mma(vA[t], df[j][t], dp);
-        }
-        if (!blk_full(q0[j], k0, causal, npre)) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            if (!elem_vis(qtok[j], k0 + crow(i, h), causal, npre)) s[i] = -__builtin_inff();
-        }
+        f32x16_t s = sacc[j];
+        const f32x16_t dp = dpacc[j];
+        if (!blk_nomask(q0[j], k0, causal, npre)) mask_key_rows(s, k0, h, jmax[j]);
         float ds[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -713,15 +848,14 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
         }
         if constexpr (!SOFTMAX) rsum[j] += tree_sum16(ds);
       }
+      if constexpr (!EARLY) read_kt();
 #pragma unroll
       for (int d = 0; d < ND; ++d)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const frag ktA = ld8<T>(sKt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h));
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int j = 0; j < QPW; ++j)
-            if (act[j]) dqacc[j][d] = E::mma(ktA, sf[j][t], dqacc[j][d]);
-        }
+            if (act[j]) dqacc[j][d] = E::mma(ktA[d][t], sf[j][t], dqacc[j][d]);
     }
   }
 
@@ -766,16 +900,19 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
 //   dP = dO V^T (init -Delta), dS = P dP,
 //   dV^T += dO^T P, dK^T += Q^T dS, colsum += sum_i dS.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int KPW, int BM, bool SOFTMAX>
+template <typename T, int DP, int W, int KPW, int BM, bool SOFTMAX, bool EARLY = true, bool PIPE = false>
 __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   constexpr int NT = 64 * W, QB = BM / 32, KS = DP / 16, ND = DP / 32, GB = W * KPW;
   constexpr int LDR = DP + E::PAD, LDT = BM + E::PAD;
+  // 16-bit types read Q^T and dO^T from the row-major tiles with transposing
+  // LDS reads; fp32 stages transposed copies.
+  constexpr bool TR = sizeof(T) == 2;
   __shared__ __attribute__((aligned(16))) T sQ[2][BM * LDR];
-  __shared__ __attribute__((aligned(16))) T sQt[2][DP * LDT];
+  __shared__ __attribute__((aligned(16))) T sQt[TR ? 1 : 2][TR ? 8 : DP * LDT];
   __shared__ __attribute__((aligned(16))) T sD[2][BM * LDR];
-  __shared__ __attribute__((aligned(16))) T sDt[2][DP * LDT];
+  __shared__ __attribute__((aligned(16))) T sDt[TR ? 1 : 2][TR ? 8 : DP * LDT];
   __shared__ __attribute__((aligned(16))) float sOff[2][BM];
   __shared__ __attribute__((aligned(16))) float sDel[2][BM];
 
@@ -803,13 +940,14 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   const int kblk0 = blk0 + wave * KPW;
   const bool wave_on = kblk0 + KPW - 1 >= 0;
 
-  int k0[KPW], ktok[KPW];
+  int k0[KPW], ktok[KPW], ilo[KPW];
   frag kf[KPW][KS], vf[KPW][KS];
   float nckn[KPW];  // -c * 0.5||k||^2
 #pragma unroll
   for (int j = 0; j < KPW; ++j) {
     k0[j] = org + 32 * (kblk0 + j);
     ktok[j] = k0[j] + n;
+    ilo[j] = first_query(ktok[j], causal, npre);
     const bool kvalid = wave_on && ktok[j] >= 0;
     float s = 0.f;
 #pragma unroll
@@ -852,7 +990,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
     if (tid < BM) {
       const int tok = tok0 + tid;
       const bool ok = tok >= 0 && tok < N;
-      offr = ok ? -offg[tok] * inv_c : 0.f;
+      offr = ok ? -offg[tok] * inv_c : -__builtin_inff();  // padding queries: P = 0
       if constexpr (SOFTMAX) delr = ok ? -delg[tok] : 0.f;
     }
   };
@@ -860,9 +998,11 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   for (int qt = qt_lo; qt < nqt_all; ++qt) {
     const int buf = qt & 1;
     tq.template store_rows<LDR>(sQ[buf], tid);
-    tq.template store_trans<LDT>(sQt[buf], tid);
     td.template store_rows<LDR>(sD[buf], tid);
-    td.template store_trans<LDT>(sDt[buf], tid);
+    if constexpr (!TR) {
+      tq.template store_trans<LDT>(sQt[buf], tid);
+      td.template store_trans<LDT>(sDt[buf], tid);
+    }
     if (tid < BM) {
       sOff[buf][tid] = offr;
       sDel[buf][tid] = delr;
@@ -871,6 +1011,65 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
     if (qt + 1 < nqt_all) load_tile(qt + 1);
     if (!wave_on) continue;
     const int qblk0 = qt * QB - qshift;
+    if constexpr (PIPE && KPW == 1) {
+      // Fast path for tiles whose every (query block, key block) pair is fully
+      // visible to this wave (the interior of the causal triangle): no
+      // branches, and software-pipelined -- the S and dP MFMAs of all QB
+      // blocks are issued first, so block qb's elementwise work overlaps the
+      // MFMAs of block qb+1 and the dV/dK MFMAs of block qb-1.
+      bool fast = true;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const int q0 = org + 32 * (qblk0 + qb);
+        fast = fast && blk_any(q0, k0[0], causal, npre) && blk_nomask(q0, k0[0], causal, npre);
+      }
+      if (fast) {
+        f32x16_t sacc[QB], dpacc[QB];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          sacc[qb] = ld_rows16(sOff[buf] + 32 * qb, h);
+          if constexpr (SOFTMAX) dpacc[qb] = ld_rows16(sDel[buf] + 32 * qb, h);
+          else dpacc[qb] = zero16();
+#pragma unroll
+          for (int t = 0; t < KS; ++t) {
+            const frag qA = ld8<T>(sQ[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h);
+            const frag dA = ld8<T>(sD[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h);
+            sacc[qb] = E::mma(qA, kf[0][t], sacc[qb]);
+            dpacc[qb] = E::mma(dA, vf[0][t], dpacc[qb]);
+          }
+        }
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          frag pf[2], sf[2];
+          float ds[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float pv = fast_exp2(fmaf(sacc[qb][i], c, nckn[0]));
+            ds[i] = pv * dpacc[qb][i];
+            pf[i >> 3][i & 7] = (T)pv;
+            sf[i >> 3][i & 7] = (T)ds[i];
+          }
+          csum[0] += tree_sum16(ds);
+#pragma unroll
+          for (int d = 0; d < ND; ++d)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              frag dtA, qtA;
+              if constexpr (TR) {
+                dtA = ld_tr8<T, LDR>(sD[buf], 32 * qb + 16 * t, 32 * d, lane);
+                qtA = ld_tr8<T, LDR>(sQ[buf], 32 * qb + 16 * t, 32 * d, lane);
+              } else {
+                const int o = (32 * d + n) * LDT + tchunk<BM>(32 * d + n, 32 * qb + 16 * t + 8 * h);
+                dtA = ld8<T>(sDt[buf] + o);
+                qtA = ld8<T>(sQt[buf] + o);
+              }
+              dvacc[0][d] = E::mma(dtA, pf[t], dvacc[0][d]);
+              dkacc[0][d] = E::mma(qtA, sf[t], dkacc[0][d]);
+            }
+        }
+        continue;
+      }
+    }
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const int q0 = org + 32 * (qblk0 + qb);
@@ -892,21 +1091,44 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
       f32x16_t dinit;
       if constexpr (SOFTMAX) dinit = ld_rows16(sDel[buf] + 32 * qb, h);
       else dinit = zero16();
+      f32x16_t sacc[KPW], dpacc[KPW];
+#pragma unroll
+      for (int j = 0; j < KPW; ++j) {
+        if (!act[j]) continue;
+        sacc[j] = oinit;
+        dpacc[j] = dinit;
+#pragma unroll
+        for (int t = 0; t < KS; ++t) {
+          sacc[j] = E::mma(qA[t], kf[j][t], sacc[j]);
+          dpacc[j] = E::mma(dA[t], vf[j][t], dpacc[j]);
+        }
+      }
+      // dO^T and Q^T fragments are read while the S / dP MFMAs and the
+      // elementwise work run.
+      frag dtA[ND][2], qtA[ND][2];
+      auto read_t = [&]() {
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            if constexpr (TR) {
+              dtA[d][t] = ld_tr8<T, LDR>(sD[buf], 32 * qb + 16 * t, 32 * d, lane);
+              qtA[d][t] = ld_tr8<T, LDR>(sQ[buf], 32 * qb + 16 * t, 32 * d, lane);
+            } else {
+              const int o = (32 * d + n) * LDT + tchunk<BM>(32 * d + n, 32 * qb + 16 * t + 8 * h);
+              dtA[d][t] = ld8<T>(sDt[buf] + o);
+              qtA[d][t] = ld8<T>(sQt[buf] + o);
+            }
+          }
+      };
+      if constexpr (EARLY) read_t();
       frag pf[KPW][2], sf[KPW][2];
 #pragma unroll
       for (int j = 0; j < KPW; ++j) {
         if (!act[j]) continue;
-        f32x16_t s = oinit, dp = dinit;
-#pragma unroll
-        for (int t = 0; t < KS; ++t) {
-          s = E::mma(qA[t], kf[j][t], s);
-          dp = E::mma(dA[t], vf[j][t], dp);
-        }
-        if (!blk_full(q0, k0[j], causal, npre)) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            if (!elem_vis(q0 + crow(i, h), ktok[j], causal, npre)) s[i] = -__builtin_inff();
-        }
+        f32x16_t s = sacc[j];
+        const f32x16_t dp = dpacc[j];
+        if (!blk_nomask(q0, k0[j], causal, npre)) mask_query_rows(s, q0, h, ilo[j]);
         float ds[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -917,20 +1139,17 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
         }
         csum[j] += tree_sum16(ds);
       }
+      if constexpr (!EARLY) read_t();
 #pragma unroll
       for (int d = 0; d < ND; ++d)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int o = (32 * d + n) * LDT + tchunk<BM>(32 * d + n, 32 * qb + 16 * t + 8 * h);
-          const frag dtA = ld8<T>(sDt[buf] + o);
-          const frag qtA = ld8<T>(sQt[buf] + o);
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int j = 0; j < KPW; ++j)
             if (act[j]) {
-              dvacc[j][d] = E::mma(dtA, pf[j][t], dvacc[j][d]);
-              dkacc[j][d] = E::mma(qtA, sf[j][t], dkacc[j][d]);
+              dvacc[j][d] = E::mma(dtA[d][t], pf[j][t], dvacc[j][d]);
+              dkacc[j][d] = E::mma(qtA[d][t], sf[j][t], dkacc[j][d]);
             }
-        }
     }
   }
 

@@ -34,22 +34,22 @@ inline unsigned grid_of(const Params& p, int blocks_per_wg) {
   return (unsigned)((long long)p.B * p.H * ngrp);
 }
 
-template <int DP, bool SM, int W, int QPW, int BN>
+template <int DP, bool SM, int W, int QPW, int BN, bool EARLY = true, int PF = 1>
 hipError_t fwd_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_fwd_kernel<Elt, DP, W, QPW, BN, SM>), dim3(grid_of(p, W * QPW)), dim3(64 * W), 0, st, p);
+  hipLaunchKernelGGL((rbf_fwd_kernel<Elt, DP, W, QPW, BN, SM, EARLY, PF>), dim3(grid_of(p, W * QPW)), dim3(64 * W), 0, st, p);
   return hipGetLastError();
 }
 
-template <int DP, bool SM, int W, int QPW, int BN>
+template <int DP, bool SM, int W, int QPW, int BN, bool EARLY = true>
 hipError_t dq_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_bwd_dq_kernel<Elt, DP, W, QPW, BN, SM>), dim3(grid_of(p, W * QPW)), dim3(64 * W), 0, st,
+  hipLaunchKernelGGL((rbf_bwd_dq_kernel<Elt, DP, W, QPW, BN, SM, EARLY>), dim3(grid_of(p, W * QPW)), dim3(64 * W), 0, st,
                      p);
   return hipGetLastError();
 }
 
-template <int DP, bool SM, int W, int KPW, int BM>
+template <int DP, bool SM, int W, int KPW, int BM, bool EARLY = true, bool PIPE = false>
 hipError_t dkdv_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_bwd_dkdv_kernel<Elt, DP, W, KPW, BM, SM>), dim3(grid_of(p, W * KPW)), dim3(64 * W), 0,
+  hipLaunchKernelGGL((rbf_bwd_dkdv_kernel<Elt, DP, W, KPW, BM, SM, EARLY, PIPE>), dim3(grid_of(p, W * KPW)), dim3(64 * W), 0,
                      st, p);
   return hipGetLastError();
 }
@@ -93,6 +93,10 @@ hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
     case 3: return fwd_cfg<DP, SM, 2, 1, 64>(p, st);
     case 4: return fwd_cfg<DP, SM, 4, 1, 128>(p, st);
     case 5: return fwd_cfg<DP, SM, 8, 1, 64>(p, st);
+    case 6: return fwd_cfg<DP, SM, 4, 1, 64, false>(p, st);
+    case 7: return fwd_cfg<DP, SM, 4, 1, 64, true, 2>(p, st);
+    case 8: return fwd_cfg<DP, SM, 4, 1, 32, true, 2>(p, st);
+    case 9: return fwd_cfg<DP, SM, 2, 1, 64, true, 2>(p, st);
     default: break;
   }
   }
@@ -112,6 +116,7 @@ hipError_t dq_any_cfg(const Params& p, hipStream_t st) {
     case 3: return dq_cfg<DP, SM, 4, 2, 32>(p, st);
     case 4: return dq_cfg<DP, SM, 4, 1, 32>(p, st);
     case 5: return dq_cfg<DP, SM, 8, 1, 64>(p, st);
+    case 6: return dq_cfg<DP, SM, 4, 1, 64, false>(p, st);
     default: break;
   }
   }
@@ -122,6 +127,14 @@ hipError_t dq_any_cfg(const Params& p, hipStream_t st) {
 template <int DP, bool SM>
 hipError_t dkdv_any_cfg(const Params& p, hipStream_t st) {
 #if RBF_ELEM_ID == 0
+  if constexpr (DP == 128) {
+    static const int choice = env_choice("RBF_ATTN_DKDV_CFG");
+    switch (choice) {
+      case 7: return dkdv_cfg<DP, SM, 4, 1, 64, true, true>(p, st);
+      case 9: return dkdv_cfg<DP, SM, 4, 1, 32, true, false>(p, st);
+      default: break;
+    }
+  }
   if constexpr (DP <= 64) {
   static const int choice = env_choice("RBF_ATTN_DKDV_CFG");
   switch (choice) {
@@ -131,6 +144,9 @@ hipError_t dkdv_any_cfg(const Params& p, hipStream_t st) {
     case 3: return dkdv_cfg<DP, SM, 4, 2, 32>(p, st);
     case 4: return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
     case 5: return dkdv_cfg<DP, SM, 8, 1, 64>(p, st);
+    case 6: return dkdv_cfg<DP, SM, 4, 1, 64, false>(p, st);
+    case 7: return dkdv_cfg<DP, SM, 4, 1, 64, true, true>(p, st);
+    case 8: return dkdv_cfg<DP, SM, 4, 1, 128, true, true>(p, st);
     default: break;
   }
   }
