@@ -60,30 +60,47 @@ int env_choice(const char* name) {
 }
 
 // ---- defaults ------------------------------------------------------------
+// Chosen from measured sweeps on MI355X (N = 516 and N = 8196, D = 64 / 128).
+// The forward switches to 8-wave work-groups over longer key tiles once a
+// head has enough tokens to keep them busy.
+constexpr int kLongSeq = 2048;
+
 template <int DP, bool SM>
 hipError_t fwd_default(const Params& p, hipStream_t st) {
   if constexpr (kIsF32) return fwd_cfg<DP, SM, 4, 1, 32>(p, st);
-  else return fwd_cfg<DP, SM, 4, 1, 64>(p, st);
+  else if constexpr (DP <= 64)
+    return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 1, 128>(p, st) : fwd_cfg<DP, SM, 4, 1, 64>(p, st);
+  else
+    return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 1, 64>(p, st) : fwd_cfg<DP, SM, 4, 1, 64>(p, st);
 }
 
 template <int DP, bool SM>
 hipError_t dq_default(const Params& p, hipStream_t st) {
   if constexpr (kIsF32) return dq_cfg<DP, SM, 4, 1, 32>(p, st);
-  else if constexpr (DP <= 64) return dq_cfg<DP, SM, 4, 1, 64>(p, st);
+  else if constexpr (DP <= 64) return dq_cfg<DP, SM, 4, 1, 128>(p, st);
   else return dq_cfg<DP, SM, 4, 1, 32>(p, st);
 }
 
 template <int DP, bool SM>
 hipError_t dkdv_default(const Params& p, hipStream_t st) {
   if constexpr (kIsF32) return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
-  else if constexpr (DP <= 64) return dkdv_cfg<DP, SM, 4, 1, 64>(p, st);
-  else return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
+  else if constexpr (DP <= 64) return dkdv_cfg<DP, SM, 4, 1, 128>(p, st);
+  else return dkdv_cfg<DP, SM, 4, 1, 64, false>(p, st);
 }
 
 // ---- tuning candidates (bf16, 32 < D <= 64) ------------------------------
 template <int DP, bool SM>
 hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
 #if RBF_ELEM_ID == 0
+  if constexpr (DP == 128) {
+    static const int choice = env_choice("RBF_ATTN_FWD_CFG");
+    switch (choice) {
+      case 8: return fwd_cfg<DP, SM, 4, 1, 32>(p, st);
+      case 9: return fwd_cfg<DP, SM, 4, 1, 64, false>(p, st);
+      case 11: return fwd_cfg<DP, SM, 8, 1, 64>(p, st);
+      default: break;
+    }
+  }
   if constexpr (DP <= 64) {
   static const int choice = env_choice("RBF_ATTN_FWD_CFG");
   switch (choice) {
@@ -97,6 +114,7 @@ hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
     case 7: return fwd_cfg<DP, SM, 4, 1, 64, true, 2>(p, st);
     case 8: return fwd_cfg<DP, SM, 4, 1, 32, true, 2>(p, st);
     case 9: return fwd_cfg<DP, SM, 2, 1, 64, true, 2>(p, st);
+    case 11: return fwd_cfg<DP, SM, 8, 1, 128>(p, st);
     default: break;
   }
   }
@@ -107,6 +125,14 @@ hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
 template <int DP, bool SM>
 hipError_t dq_any_cfg(const Params& p, hipStream_t st) {
 #if RBF_ELEM_ID == 0
+  if constexpr (DP == 128) {
+    static const int choice = env_choice("RBF_ATTN_DQ_CFG");
+    switch (choice) {
+      case 8: return dq_cfg<DP, SM, 4, 1, 64>(p, st);
+      case 9: return dq_cfg<DP, SM, 4, 1, 32, false>(p, st);
+      default: break;
+    }
+  }
   if constexpr (DP <= 64) {
   static const int choice = env_choice("RBF_ATTN_DQ_CFG");
   switch (choice) {
@@ -117,6 +143,8 @@ hipError_t dq_any_cfg(const Params& p, hipStream_t st) {
     case 4: return dq_cfg<DP, SM, 4, 1, 32>(p, st);
     case 5: return dq_cfg<DP, SM, 8, 1, 64>(p, st);
     case 6: return dq_cfg<DP, SM, 4, 1, 64, false>(p, st);
+    case 8: return dq_cfg<DP, SM, 4, 1, 128>(p, st);
+    case 11: return dq_cfg<DP, SM, 8, 1, 64>(p, st);
     default: break;
   }
   }
@@ -131,7 +159,9 @@ hipError_t dkdv_any_cfg(const Params& p, hipStream_t st) {
     static const int choice = env_choice("RBF_ATTN_DKDV_CFG");
     switch (choice) {
       case 7: return dkdv_cfg<DP, SM, 4, 1, 64, true, true>(p, st);
-      case 9: return dkdv_cfg<DP, SM, 4, 1, 32, true, false>(p, st);
+      case 8: return dkdv_cfg<DP, SM, 4, 1, 64, true, false>(p, st);
+      case 9: return dkdv_cfg<DP, SM, 4, 1, 32, false, false>(p, st);
+      case 10: return dkdv_cfg<DP, SM, 4, 1, 64, false, false>(p, st);
       default: break;
     }
   }
@@ -146,7 +176,9 @@ hipError_t dkdv_any_cfg(const Params& p, hipStream_t st) {
     case 5: return dkdv_cfg<DP, SM, 8, 1, 64>(p, st);
     case 6: return dkdv_cfg<DP, SM, 4, 1, 64, false>(p, st);
     case 7: return dkdv_cfg<DP, SM, 4, 1, 64, true, true>(p, st);
-    case 8: return dkdv_cfg<DP, SM, 4, 1, 128, true, true>(p, st);
+    case 8: return dkdv_cfg<DP, SM, 4, 1, 128, true, false>(p, st);
+    case 10: return dkdv_cfg<DP, SM, 4, 1, 128, false, false>(p, st);
+    case 11: return dkdv_cfg<DP, SM, 8, 1, 128, true, false>(p, st);
     default: break;
   }
   }
