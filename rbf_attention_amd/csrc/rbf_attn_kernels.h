@@ -458,20 +458,37 @@ __device__ inline f32x16_t splat16(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// Forward.  A wave owns QPW consecutive 32-query blocks, a work-group W
-// waves; BN-key tiles of K (row-major), V (transposed) and -0.5||k||^2 stream
-// through double-buffered LDS.  Per 32-key block the wave reads the K, V^T
-// fragments and key norms once and reuses them for its QPW query blocks:
+// Forward.  A wave owns one 32-query block, a work-group W waves; BN-key
+// tiles of K (row-major), V and -0.5||k||^2 stream through double-buffered
+// LDS.  Per 32-key block:
 //   S^T = K Q^T (accumulator initialised with -0.5||k||^2),
-//   P   = exp2(c S^T - m) with a lazily raised running max m,
-//   O^T += V^T P^T.
+//   P   = exp2(c S^T - m),
+//   O^T += V^T P^T, and l += 1^T P^T on the same MFMA path (an operand whose
+//   first row is ones), so the softmax denominator sums exactly the
+//   bf16-rounded P the numerator uses.
+// Softmax offset m: every RBF logit obeys c(q.k - 0.5||k||^2) <= c 0.5||q||^2,
+// so m = c 0.5||q||^2 - 60 bounds P by 2^60 without any running max.  If some
+// row's keys all lie so far away that its sum falls below 2^-60 (or the sum is
+// not finite), the work-group reruns with an online, lazily raised max.  fp16
+// cannot hold P up to 2^60 and always takes the online max.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX, bool EARLY = true, int PF = 1>
+template <typename T>
+__device__ inline typename Elem<T>::frag ones_row_frag(int n) {
+  typename Elem<T>::frag f;
+  const T v = (T)(n == 0 ? 1.f : 0.f);
+#pragma unroll
+  for (int s = 0; s < 8; ++s) f[s] = v;
+  return f;
+}
+
+constexpr float kBoundMargin = 60.f;  // P <= 2^60 under the static bound
+constexpr float kSumLow = 0x1p-60f, kSumHigh = 0x1p100f;
+
+template <typename T, int DP, int W, int BN, bool SOFTMAX>
 __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
-  static_assert(PF == 1 || PF == 2, "prefetch depth is 1 or 2 tiles");
   typedef Elem<T> E;
   typedef typename E::frag frag;
-  constexpr int NT = 64 * W, KB = BN / 32, KS = DP / 16, ND = DP / 32, GB = W * QPW;
+  constexpr int NT = 64 * W, KB = BN / 32, KS = DP / 16, ND = DP / 32;
   constexpr int LDR = DP + E::PAD, LDT = BN + E::PAD;
   // 16-bit types keep V row-major and read V^T with transposing LDS reads;
   // fp32 stages a transposed copy.
@@ -486,7 +503,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   const bool causal = p.causal != 0;
   const int npre = p.num_prefix;
   const float c = p.c;
-  const int ngrp = (nblk + GB - 1) / GB;
+  const int ngrp = (nblk + W - 1) / W;
   int bh, grp;
   decode_wg(ngrp, causal, bh, grp);
   const int b = bh / p.H, hh = bh - b * p.H;
@@ -495,10 +512,14 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   const T* V = reinterpret_cast<const T*>(p.v) + b * p.sv[0] + hh * p.sv[1];
   T* O = reinterpret_cast<T*>(const_cast<void*>(p.o)) + b * p.so[0] + hh * p.so[1];
 
-  const int blk0 = nblk - (ngrp - grp) * GB;
-  const int qblk0 = blk0 + wave * QPW;            // first query block of this wave
-  const bool wave_on = qblk0 + QPW - 1 >= 0;      // its last block holds real queries
-  const int wg_qlast = org + 32 * (blk0 + GB) - 1;
+  const int blk0 = nblk - (ngrp - grp) * W;
+  const int qblk = blk0 + wave;
+  const bool wave_on = qblk >= 0;  // the wave's block holds real queries
+  const int q0 = org + 32 * qblk;
+  const int qtok = q0 + n;
+  const bool qvalid = wave_on && qtok >= 0;
+  const int jmax = last_key(qtok, N, causal, npre);
+  const int wg_qlast = org + 32 * (blk0 + W) - 1;
   int hi = causal ? max(wg_qlast + 1, npre) : N;
   hi = min(hi, N);
   const int nkt_all = (nblk + KB - 1) / KB;
@@ -506,84 +527,57 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   const int last_blk = (hi - 1 - org) >> 5;
   const int nkt = (last_blk + kshift) / KB + 1;
 
-  int q0[QPW], qtok[QPW], jmax[QPW];
-  frag qf[QPW][KS];
-  float qoff[QPW];
+  frag qf[KS];
+  float qn2 = 0.f;  // c * 0.5 ||q||^2
 #pragma unroll
-  for (int j = 0; j < QPW; ++j) {
-    q0[j] = org + 32 * (qblk0 + j);
-    qtok[j] = q0[j] + n;
-    jmax[j] = last_key(qtok[j], N, causal, npre);
-    const bool ok = wave_on && qtok[j] >= 0;
-#pragma unroll
-    for (int t = 0; t < KS; ++t)
-      qf[j][t] = (ok && 16 * t + 8 * h < D) ? ld8<T>(Q + (int64_t)qtok[j] * p.sq[2] + 16 * t + 8 * h) : zero_frag<T>();
-    qoff[j] = 0.f;
-    if constexpr (!SOFTMAX) {
-      float s = 0.f;
-#pragma unroll
-      for (int t = 0; t < KS; ++t) s += sumsq8<T>(qf[j][t]);
-      s = xhalf_sum(s);
-      qoff[j] = c * 0.5f * s;
-    }
+  for (int t = 0; t < KS; ++t) {
+    qf[t] = (qvalid && 16 * t + 8 * h < D) ? ld8<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h) : zero_frag<T>();
+    qn2 += sumsq8<T>(qf[t]);
   }
+  qn2 = c * 0.5f * xhalf_sum(qn2);
+  const frag onesA = ones_row_frag<T>(n);
 
-  f32x16_t oacc[QPW][ND];
-  float m_run[QPW], l_run[QPW];
-#pragma unroll
-  for (int j = 0; j < QPW; ++j) {
-#pragma unroll
-    for (int d = 0; d < ND; ++d) oacc[j][d] = zero16();
-    m_run[j] = -__builtin_inff();
-    l_run[j] = 0.f;
-  }
+  f32x16_t oacc[ND], lacc;
+  float m_run;
 
-  // Key tiles are staged global -> registers -> LDS.  With PF = 2 two
-  // register sets alternate, so the global loads of tile kt+2 are in flight
-  // while tile kt is computed and tile kt+1 waits in registers.
   typedef Tile<T, BN, DP, NT> TileT;
-  auto load_kv = [&](int kt, TileT& tk, TileT& tv) {
+  TileT tk, tv;
+  auto load_kv = [&](int kt) {
     const int tok0 = org + 32 * (kt * KB - kshift);
     tk.load(K, p.sk[2], tok0, N, D, tid);
     tv.load(V, p.sv[2], tok0, N, D, tid);
   };
-  auto tile_step = [&](int kt, TileT& tk, TileT& tv) {
-    const int buf = kt & 1;
-    tk.template store_rows<LDR>(sK[buf], tid);
-    tk.store_neg_halfnorm(sKn[buf], tid);
-    if constexpr (TR) tv.template store_rows<LDR>(sVt[buf], tid);
-    else tv.template store_trans<LDT>(sVt[buf], tid);
-    __syncthreads();
-    if (kt + PF < nkt) load_kv(kt + PF, tk, tv);
-    if (!wave_on) return;
-    const int kblk0 = kt * KB - kshift;
+
+  // One pass over the key tiles.  SAFE = online max with lazy rescaling.
+  auto run = [&](auto safe_tag) {
+    constexpr bool SAFE = decltype(safe_tag)::value;
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      const int k0 = org + 32 * (kblk0 + kb);
-      bool act[QPW];
-      bool any = false;
+    for (int d = 0; d < ND; ++d) oacc[d] = zero16();
+    lacc = zero16();
+    m_run = !SOFTMAX ? qn2 : (SAFE ? -__builtin_inff() : qn2 - kBoundMargin);
+    load_kv(0);
+    for (int kt = 0; kt < nkt; ++kt) {
+      const int buf = kt & 1;
+      tk.template store_rows<LDR>(sK[buf], tid);
+      tk.store_neg_halfnorm(sKn[buf], tid);
+      if constexpr (TR) tv.template store_rows<LDR>(sVt[buf], tid);
+      else tv.template store_trans<LDT>(sVt[buf], tid);
+      __syncthreads();
+      if (kt + 1 < nkt) load_kv(kt + 1);
+      if (!wave_on) continue;
+      const int kblk0 = kt * KB - kshift;
 #pragma unroll
-      for (int j = 0; j < QPW; ++j) {
-        act[j] = blk_any(q0[j], k0, causal, npre);
-        any = any || act[j];
-      }
-      if (!any) continue;
-      frag kA[KS];
+      for (int kb = 0; kb < KB; ++kb) {
+        const int k0 = org + 32 * (kblk0 + kb);
+        if (!blk_any(q0, k0, causal, npre)) continue;
+        frag kA[KS];
 #pragma unroll
-      for (int t = 0; t < KS; ++t) kA[t] = ld8<T>(sK[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h);
-      const f32x16_t kinit = ld_rows16(sKn[buf] + 32 * kb, h);
-      f32x16_t sacc[QPW];
+        for (int t = 0; t < KS; ++t) kA[t] = ld8<T>(sK[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h);
+        f32x16_t s = ld_rows16(sKn[buf] + 32 * kb, h);
 #pragma unroll
-      for (int j = 0; j < QPW; ++j) {
-        if (!act[j]) continue;
-        sacc[j] = kinit;
-#pragma unroll
-        for (int t = 0; t < KS; ++t) sacc[j] = E::mma(kA[t], qf[j][t], sacc[j]);
-      }
-      // V^T fragments are read while the S MFMAs and the softmax run (EARLY),
-      // or next to the P.V MFMAs.
-      frag vA[ND][2];
-      auto read_v = [&]() {
+        for (int t = 0; t < KS; ++t) s = E::mma(kA[t], qf[t], s);
+        // V^T fragments are read while the S MFMAs and the softmax run.
+        frag vA[ND][2];
 #pragma unroll
         for (int d = 0; d < ND; ++d)
 #pragma unroll
@@ -591,83 +585,67 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
             if constexpr (TR) vA[d][t] = ld_tr8<T, LDR>(sVt[buf], 32 * kb + 16 * t, 32 * d, lane);
             else vA[d][t] = ld8<T>(sVt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h));
           }
-      };
-      if constexpr (EARLY) read_v();
-      frag pf[QPW][2];
+        if (!blk_nomask(q0, k0, causal, npre)) mask_key_rows(s, k0, h, jmax);
+        if constexpr (SOFTMAX && SAFE) {
+          const float mt = xhalf_max(tree_max16(s)) * c;
+          if (__any(mt > m_run + kTau)) {
+            const float mnew = fmaxf(m_run, mt);
+            const float alpha = (mnew == -__builtin_inff()) ? 1.f : fast_exp2(m_run - mnew);
 #pragma unroll
-      for (int j = 0; j < QPW; ++j) {
-        if (!act[j]) continue;
-        f32x16_t s = sacc[j];
-        if (!blk_nomask(q0[j], k0, causal, npre)) mask_key_rows(s, k0, h, jmax[j]);
-        float moff;
-        if constexpr (SOFTMAX) {
-          const float mx = xhalf_max(tree_max16(s));
-          const float mt = mx * c;
-          if (__any(mt > m_run[j] + kTau)) {
-            const float mnew = fmaxf(m_run[j], mt);
-            const float alpha = (mnew == -__builtin_inff()) ? 1.f : fast_exp2(m_run[j] - mnew);
-            l_run[j] *= alpha;
-#pragma unroll
-            for (int d = 0; d < ND; ++d) oacc[j][d] *= alpha;
-            m_run[j] = mnew;
+            for (int d = 0; d < ND; ++d) oacc[d] *= alpha;
+            lacc *= alpha;
+            m_run = mnew;
           }
-          moff = (m_run[j] == -__builtin_inff()) ? 0.f : m_run[j];
-        } else {
-          moff = qoff[j];
         }
-        float pv[16];
+        const float moff = (SAFE && m_run == -__builtin_inff()) ? 0.f : m_run;
+        frag pf[2];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          pv[i] = fast_exp2(fmaf(s[i], c, -moff));
-          pf[j][i >> 3][i & 7] = (T)pv[i];
+        for (int i = 0; i < 16; ++i) pf[i >> 3][i & 7] = (T)fast_exp2(fmaf(s[i], c, -moff));
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+          for (int d = 0; d < ND; ++d) oacc[d] = E::mma(vA[d][t], pf[t], oacc[d]);
+          if constexpr (SOFTMAX) lacc = E::mma(onesA, pf[t], lacc);
         }
-        if constexpr (SOFTMAX) l_run[j] += tree_sum16(pv);
       }
-      if constexpr (!EARLY) read_v();
-#pragma unroll
-      for (int d = 0; d < ND; ++d)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int j = 0; j < QPW; ++j)
-            if (act[j]) oacc[j][d] = E::mma(vA[d][t], pf[j][t], oacc[j][d]);
     }
   };
-  TileT tkA, tvA;
-  load_kv(0, tkA, tvA);
-  if constexpr (PF == 1) {
-    for (int kt = 0; kt < nkt; ++kt) tile_step(kt, tkA, tvA);
+
+  constexpr bool STATIC = SOFTMAX && !std::is_same<T, _Float16>::value;
+  if constexpr (SOFTMAX && !STATIC) {
+    run(std::true_type{});
   } else {
-    TileT tkB, tvB;
-    if (nkt > 1) load_kv(1, tkB, tvB);
-    for (int kt = 0; kt < nkt; kt += 2) {
-      tile_step(kt, tkA, tvA);
-      if (kt + 1 < nkt) tile_step(kt + 1, tkB, tvB);
+    run(std::false_type{});
+  }
+  if constexpr (STATIC) {
+    // lacc row 0 (element 0 of the h = 0 lanes) is the row sum; the h = 1
+    // lanes hold row 4, which is zero.
+    const float l = xhalf_sum(lacc[0]);
+    const bool bad = qvalid && !(l >= kSumLow && l <= kSumHigh);
+    if (__syncthreads_or(bad)) {
+      __syncthreads();  // every wave is done reading the last tile
+      run(std::true_type{});
     }
   }
 
   if (!wave_on) return;
+  const float lsum = SOFTMAX ? xhalf_sum(lacc[0]) : 1.f;
+  const float inv = SOFTMAX ? 1.f / lsum : 1.f;
+  if (qtok < 0) return;
+  T* orow = O + (int64_t)qtok * p.so[2];
 #pragma unroll
-  for (int j = 0; j < QPW; ++j) {
-    float lsum = l_run[j];
-    if constexpr (SOFTMAX) lsum = xhalf_sum(lsum);
-    const float inv = SOFTMAX ? 1.f / lsum : 1.f;
-    if (qtok[j] < 0) continue;
-    T* orow = O + (int64_t)qtok[j] * p.so[2];
+  for (int d = 0; d < ND; ++d)
 #pragma unroll
-    for (int d = 0; d < ND; ++d)
+    for (int g = 0; g < 4; ++g) {
+      const int dd = 32 * d + 8 * g + 4 * h;
+      if (dd < D) {
+        float v4[4];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int dd = 32 * d + 8 * g + 4 * h;
-        if (dd < D) {
-          float v4[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v4[e] = oacc[j][d][4 * g + e] * inv;
-          st4f<T>(orow + dd, v4);
-        }
+        for (int e = 0; e < 4; ++e) v4[e] = oacc[d][4 * g + e] * inv;
+        st4f<T>(orow + dd, v4);
       }
-    if (SOFTMAX && h == 0) p.lse[(int64_t)bh * N + qtok[j]] = m_run[j] + __log2f(lsum);
-  }
+    }
+  if (SOFTMAX && h == 0) p.lse[(int64_t)bh * N + qtok] = m_run + __log2f(lsum);
 }
 
 // ---------------------------------------------------------------------------
@@ -900,7 +878,8 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
 //   dP = dO V^T (init -Delta), dS = P dP,
 //   dV^T += dO^T P, dK^T += Q^T dS, colsum += sum_i dS.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int KPW, int BM, bool SOFTMAX, bool EARLY = true, bool PIPE = false>
+template <typename T, int DP, int W, int KPW, int BM, bool SOFTMAX, bool EARLY = true, bool PIPE = false,
+          bool PRIO = false>
 __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -1092,6 +1071,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
       if constexpr (SOFTMAX) dinit = ld_rows16(sDel[buf] + 32 * qb, h);
       else dinit = zero16();
       f32x16_t sacc[KPW], dpacc[KPW];
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int j = 0; j < KPW; ++j) {
         if (!act[j]) continue;
@@ -1103,6 +1083,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
           dpacc[j] = E::mma(dA[t], vf[j][t], dpacc[j]);
         }
       }
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
       // dO^T and Q^T fragments are read while the S / dP MFMAs and the
       // elementwise work run.
       frag dtA[ND][2], qtA[ND][2];
@@ -1140,6 +1121,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
         csum[j] += tree_sum16(ds);
       }
       if constexpr (!EARLY) read_t();
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int d = 0; d < ND; ++d)
 #pragma unroll
@@ -1150,6 +1132,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
               dvacc[j][d] = E::mma(dtA[d][t], pf[j][t], dvacc[j][d]);
               dkacc[j][d] = E::mma(qtA[d][t], sf[j][t], dkacc[j][d]);
             }
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     }
   }
 
@@ -1180,6 +1163,215 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
         }
       }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, key-stationary, two waves per key block (16-bit types).  A
+// work-group holds NP key blocks and 2*NP waves: wave j (< NP) is the P-wave
+// of key block j, wave NP + j its dS-wave, and the hardware places the two on
+// the same SIMD.  Each holds half of the key block's state (K and dV, or V and
+// dK), which halves the registers per wave and lets the exponential work of
+// one wave overlap the MFMAs of the other.  Per BM-query tile:
+//   phase 1  P-wave:  S = Q K^T (init -L/c), P = exp2(c S - c*0.5||k||^2),
+//                     P -> LDS
+//            dS-wave: dP = dO V^T (init -Delta)
+//   barrier
+//   phase 2  P-wave:  dV^T += dO^T P
+//            dS-wave: dS = P dP with P from LDS, dK^T += Q^T dS, colsum += dS
+// The dS-wave takes P as rounded to the element type, the precision at which
+// P also enters dV.
+// ---------------------------------------------------------------------------
+template <typename T, int DP, int NP, int BM, bool SOFTMAX>
+__global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Params p) {
+  typedef Elem<T> E;
+  typedef typename E::frag frag;
+  static_assert(sizeof(T) == 2, "the paired kernel reads transposed operands with ds_read_b64_tr_b16");
+  constexpr int W = 2 * NP, NT = 64 * W, QB = BM / 32, KS = DP / 16, ND = DP / 32;
+  constexpr int LDR = DP + E::PAD;
+  __shared__ __attribute__((aligned(16))) T sQ[2][BM * LDR];
+  __shared__ __attribute__((aligned(16))) T sD[2][BM * LDR];
+  __shared__ __attribute__((aligned(16))) float sOff[2][BM];
+  __shared__ __attribute__((aligned(16))) float sDel[2][BM];
+  __shared__ __attribute__((aligned(16))) T sP[NP][QB][2 * 64 * 8];
+
+  const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool pwave = wave < NP;
+  const int j = pwave ? wave : wave - NP;
+  const int N = p.N, D = p.D, org = p.org, nblk = p.nblk;
+  const bool causal = p.causal != 0;
+  const int npre = p.num_prefix;
+  const float c = p.c;
+  const float inv_c = 1.f / c;
+  const int ngrp = (nblk + NP - 1) / NP;
+  int bh, grp;
+  decode_wg(ngrp, false, bh, grp);
+  const int b = bh / p.H, hh = bh - b * p.H;
+  const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
+  const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
+  const T* V = reinterpret_cast<const T*>(p.v) + b * p.sv[0] + hh * p.sv[1];
+  const T* dO = reinterpret_cast<const T*>(p.dout) + b * p.sdo[0] + hh * p.sdo[1];
+  const float* offg = p.lse + (int64_t)bh * N;
+  const float* delg = SOFTMAX ? p.delta + (int64_t)bh * N : nullptr;
+
+  const int blk0 = nblk - (ngrp - grp) * NP;
+  const int kblk = blk0 + j;
+  const bool wave_on = kblk >= 0;
+  const int k0 = org + 32 * kblk;
+  const int ktok = k0 + n;
+  const bool kvalid = wave_on && ktok >= 0;
+  const int ilo = first_query(ktok, causal, npre);
+
+  // P-wave: K fragments and -c*0.5||k||^2; dS-wave: V fragments.
+  frag kv[KS];
+  float nckn = 0.f;
+  {
+    const T* src = pwave ? K + (int64_t)ktok * p.sk[2] : V + (int64_t)ktok * p.sv[2];
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      kv[t] = (kvalid && 16 * t + 8 * h < D) ? ld8<T>(src + 16 * t + 8 * h) : zero_frag<T>();
+      s += sumsq8<T>(kv[t]);
+    }
+    nckn = -c * 0.5f * xhalf_sum(s);
+  }
+
+  f32x16_t acc[ND];  // dV^T (P-wave) or dK^T (dS-wave)
+#pragma unroll
+  for (int d = 0; d < ND; ++d) acc[d] = zero16();
+  float csum = 0.f;
+
+  const int wg_kfirst = max(org + 32 * max(blk0, 0), 0);
+  const int qlo = causal ? (wg_kfirst < npre ? 0 : wg_kfirst) : 0;
+  const int nqt_all = (nblk + QB - 1) / QB;
+  const int qshift = nqt_all * QB - nblk;
+  const int qt_lo = (((qlo - org) >> 5) + qshift) / QB;
+
+  Tile<T, BM, DP, NT> tq, td;
+  float offr = 0.f, delr = 0.f;
+  auto load_tile = [&](int qt) {
+    const int tok0 = org + 32 * (qt * QB - qshift);
+    tq.load(Q, p.sq[2], tok0, N, D, tid);
+    td.load(dO, p.sdo[2], tok0, N, D, tid);
+    if (tid < BM) {
+      const int tok = tok0 + tid;
+      const bool ok = tok >= 0 && tok < N;
+      offr = ok ? -offg[tok] * inv_c : -__builtin_inff();  // padding queries: P = 0
+      if constexpr (SOFTMAX) delr = ok ? -delg[tok] : 0.f;
+    }
+  };
+  // The two roles run separate copies of the tile loop (same trip count, same
+  // two barriers per tile), so that the compiler allocates registers for each
+  // role on its own.
+  auto tile_loop = [&](auto role) {
+    constexpr bool PW = decltype(role)::value;
+    load_tile(qt_lo);
+    for (int qt = qt_lo; qt < nqt_all; ++qt) {
+      const int buf = qt & 1;
+      tq.template store_rows<LDR>(sQ[buf], tid);
+      td.template store_rows<LDR>(sD[buf], tid);
+      if (tid < BM) {
+        sOff[buf][tid] = offr;
+        sDel[buf][tid] = delr;
+      }
+      __syncthreads();
+      if (qt + 1 < nqt_all) load_tile(qt + 1);
+      const int qblk0 = qt * QB - qshift;
+      bool act[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) act[qb] = wave_on && blk_any(org + 32 * (qblk0 + qb), k0, causal, npre);
+      if constexpr (PW) {
+        // phase 1: S, P -> registers and LDS
+        frag pf[QB][2];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          if (!act[qb]) continue;
+          const int q0 = org + 32 * (qblk0 + qb);
+          f32x16_t s = ld_rows16(sOff[buf] + 32 * qb, h);
+#pragma unroll
+          for (int t = 0; t < KS; ++t) s = E::mma(ld8<T>(sQ[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h), kv[t], s);
+          if (!blk_nomask(q0, k0, causal, npre)) mask_query_rows(s, q0, h, ilo);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) pf[qb][i >> 3][i & 7] = (T)fast_exp2(fmaf(s[i], c, nckn));
+          st8<T>(sP[j][qb] + lane * 8, pf[qb][0]);
+          st8<T>(sP[j][qb] + (64 + lane) * 8, pf[qb][1]);
+        }
+        __syncthreads();
+        // phase 2: dV^T += dO^T P
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          if (!act[qb]) continue;
+#pragma unroll
+          for (int d = 0; d < ND; ++d)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+              acc[d] = E::mma(ld_tr8<T, LDR>(sD[buf], 32 * qb + 16 * t, 32 * d, lane), pf[qb][t], acc[d]);
+        }
+      } else {
+        // phase 1: dP
+        f32x16_t dpacc[QB];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          if (!act[qb]) continue;
+          f32x16_t dp;
+          if constexpr (SOFTMAX) dp = ld_rows16(sDel[buf] + 32 * qb, h);
+          else dp = zero16();
+#pragma unroll
+          for (int t = 0; t < KS; ++t) dp = E::mma(ld8<T>(sD[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h), kv[t], dp);
+          dpacc[qb] = dp;
+        }
+        __syncthreads();
+        // phase 2: dS = P dP, dK^T += Q^T dS
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          if (!act[qb]) continue;
+          const frag p0 = ld8<T>(sP[j][qb] + lane * 8), p1 = ld8<T>(sP[j][qb] + (64 + lane) * 8);
+          frag sf[2];
+          float ds[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            ds[i] = (float)(i < 8 ? p0[i] : p1[i - 8]) * dpacc[qb][i];
+            sf[i >> 3][i & 7] = (T)ds[i];
+          }
+          csum += tree_sum16(ds);
+#pragma unroll
+          for (int d = 0; d < ND; ++d)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+              acc[d] = E::mma(ld_tr8<T, LDR>(sQ[buf], 32 * qb + 16 * t, 32 * d, lane), sf[t], acc[d]);
+        }
+      }
+    }
+  };
+  if (pwave) tile_loop(std::true_type{});
+  else tile_loop(std::false_type{});
+
+  if (!wave_on) return;
+  const float g2 = 2.f * p.gamma;
+  const float cs = xhalf_sum(csum);
+  if (ktok < 0) return;
+  T* orow = pwave ? reinterpret_cast<T*>(p.dv) + b * p.sdv[0] + hh * p.sdv[1] + (int64_t)ktok * p.sdv[2]
+                  : reinterpret_cast<T*>(p.dk) + b * p.sdk[0] + hh * p.sdk[1] + (int64_t)ktok * p.sdk[2];
+  const T* krow = K + (int64_t)ktok * p.sk[2];
+#pragma unroll
+  for (int d = 0; d < ND; ++d)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int dd = 32 * d + 8 * g + 4 * h;
+      if (dd < D) {
+        float a4[4];
+        if (pwave) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a4[e] = acc[d][4 * g + e];
+        } else {
+          float k4[4];
+          ld4f<T>(krow + dd, k4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a4[e] = g2 * (acc[d][4 * g + e] - cs * k4[e]);
+        }
+        st4f<T>(orow + dd, a4);
+      }
+    }
 }
 
 }  // namespace rbf

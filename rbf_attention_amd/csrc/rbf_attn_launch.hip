@@ -34,9 +34,9 @@ inline unsigned grid_of(const Params& p, int blocks_per_wg) {
   return (unsigned)((long long)p.B * p.H * ngrp);
 }
 
-template <int DP, bool SM, int W, int QPW, int BN, bool EARLY = true, int PF = 1>
+template <int DP, bool SM, int W, int BN>
 hipError_t fwd_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_fwd_kernel<Elt, DP, W, QPW, BN, SM, EARLY, PF>), dim3(grid_of(p, W * QPW)), dim3(64 * W), 0, st, p);
+  hipLaunchKernelGGL((rbf_fwd_kernel<Elt, DP, W, BN, SM>), dim3(grid_of(p, W)), dim3(64 * W), 0, st, p);
   return hipGetLastError();
 }
 
@@ -47,10 +47,16 @@ hipError_t dq_cfg(const Params& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int DP, bool SM, int W, int KPW, int BM, bool EARLY = true, bool PIPE = false>
+template <int DP, bool SM, int W, int KPW, int BM, bool EARLY = true, bool PIPE = false, bool PRIO = false>
 hipError_t dkdv_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_bwd_dkdv_kernel<Elt, DP, W, KPW, BM, SM, EARLY, PIPE>), dim3(grid_of(p, W * KPW)), dim3(64 * W), 0,
-                     st, p);
+  hipLaunchKernelGGL((rbf_bwd_dkdv_kernel<Elt, DP, W, KPW, BM, SM, EARLY, PIPE, PRIO>),
+                     dim3(grid_of(p, W * KPW)), dim3(64 * W), 0, st, p);
+  return hipGetLastError();
+}
+
+template <int DP, bool SM, int NP, int BM>
+hipError_t dkdv_pair_cfg(const Params& p, hipStream_t st) {
+  hipLaunchKernelGGL((rbf_bwd_dkdv_pair_kernel<Elt, DP, NP, BM, SM>), dim3(grid_of(p, NP)), dim3(128 * NP), 0, st, p);
   return hipGetLastError();
 }
 
@@ -67,11 +73,11 @@ constexpr int kLongSeq = 2048;
 
 template <int DP, bool SM>
 hipError_t fwd_default(const Params& p, hipStream_t st) {
-  if constexpr (kIsF32) return fwd_cfg<DP, SM, 4, 1, 32>(p, st);
+  if constexpr (kIsF32) return fwd_cfg<DP, SM, 4, 32>(p, st);
   else if constexpr (DP <= 64)
-    return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 1, 128>(p, st) : fwd_cfg<DP, SM, 4, 1, 64>(p, st);
+    return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 128>(p, st) : fwd_cfg<DP, SM, 4, 64>(p, st);
   else
-    return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 1, 64>(p, st) : fwd_cfg<DP, SM, 4, 1, 64>(p, st);
+    return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 64>(p, st) : fwd_cfg<DP, SM, 4, 64>(p, st);
 }
 
 template <int DP, bool SM>
@@ -85,38 +91,21 @@ template <int DP, bool SM>
 hipError_t dkdv_default(const Params& p, hipStream_t st) {
   if constexpr (kIsF32) return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
   else if constexpr (DP <= 64) return dkdv_cfg<DP, SM, 4, 1, 128>(p, st);
-  else return dkdv_cfg<DP, SM, 4, 1, 64, false>(p, st);
+  else return dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
 }
 
 // ---- tuning candidates (bf16, 32 < D <= 64) ------------------------------
 template <int DP, bool SM>
 hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
 #if RBF_ELEM_ID == 0
-  if constexpr (DP == 128) {
-    static const int choice = env_choice("RBF_ATTN_FWD_CFG");
-    switch (choice) {
-      case 8: return fwd_cfg<DP, SM, 4, 1, 32>(p, st);
-      case 9: return fwd_cfg<DP, SM, 4, 1, 64, false>(p, st);
-      case 11: return fwd_cfg<DP, SM, 8, 1, 64>(p, st);
-      default: break;
-    }
-  }
-  if constexpr (DP <= 64) {
   static const int choice = env_choice("RBF_ATTN_FWD_CFG");
   switch (choice) {
-    case 0: return fwd_cfg<DP, SM, 4, 1, 64>(p, st);
-    case 1: return fwd_cfg<DP, SM, 2, 2, 64>(p, st);
-    case 2: return fwd_cfg<DP, SM, 4, 2, 64>(p, st);
-    case 3: return fwd_cfg<DP, SM, 2, 1, 64>(p, st);
-    case 4: return fwd_cfg<DP, SM, 4, 1, 128>(p, st);
-    case 5: return fwd_cfg<DP, SM, 8, 1, 64>(p, st);
-    case 6: return fwd_cfg<DP, SM, 4, 1, 64, false>(p, st);
-    case 7: return fwd_cfg<DP, SM, 4, 1, 64, true, 2>(p, st);
-    case 8: return fwd_cfg<DP, SM, 4, 1, 32, true, 2>(p, st);
-    case 9: return fwd_cfg<DP, SM, 2, 1, 64, true, 2>(p, st);
-    case 11: return fwd_cfg<DP, SM, 8, 1, 128>(p, st);
+    case 0: return fwd_cfg<DP, SM, 4, 64>(p, st);
+    case 1: return fwd_cfg<DP, SM, 8, 128>(p, st);
+    case 2: return fwd_cfg<DP, SM, 8, 64>(p, st);
+    case 3: return fwd_cfg<DP, SM, 4, 128>(p, st);
+    case 4: return fwd_cfg<DP, SM, 2, 64>(p, st);
     default: break;
-  }
   }
 #endif
   return fwd_default<DP, SM>(p, st);
@@ -162,6 +151,11 @@ hipError_t dkdv_any_cfg(const Params& p, hipStream_t st) {
       case 8: return dkdv_cfg<DP, SM, 4, 1, 64, true, false>(p, st);
       case 9: return dkdv_cfg<DP, SM, 4, 1, 32, false, false>(p, st);
       case 10: return dkdv_cfg<DP, SM, 4, 1, 64, false, false>(p, st);
+      case 12: return dkdv_cfg<DP, SM, 4, 1, 64, false, false, true>(p, st);
+      case 20: return dkdv_pair_cfg<DP, SM, 4, 64>(p, st);
+      case 21: return dkdv_pair_cfg<DP, SM, 4, 32>(p, st);
+      case 22: return dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
+      case 23: return dkdv_pair_cfg<DP, SM, 2, 32>(p, st);
       default: break;
     }
   }
@@ -179,6 +173,12 @@ hipError_t dkdv_any_cfg(const Params& p, hipStream_t st) {
     case 8: return dkdv_cfg<DP, SM, 4, 1, 128, true, false>(p, st);
     case 10: return dkdv_cfg<DP, SM, 4, 1, 128, false, false>(p, st);
     case 11: return dkdv_cfg<DP, SM, 8, 1, 128, true, false>(p, st);
+    case 12: return dkdv_cfg<DP, SM, 4, 1, 128, true, false, true>(p, st);
+    case 20: return dkdv_pair_cfg<DP, SM, 4, 64>(p, st);
+    case 21: return dkdv_pair_cfg<DP, SM, 4, 32>(p, st);
+    case 22: return dkdv_pair_cfg<DP, SM, 4, 128>(p, st);
+    case 23: return dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
+    case 24: return dkdv_pair_cfg<DP, SM, 2, 128>(p, st);
     default: break;
   }
   }

@@ -188,11 +188,12 @@ def test_head_dims(cuda_device, D):
     compare_case(q, k, v, do, tag=f"D{D}")
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("softmax", [True, False])
-def test_dtypes(cuda_device, dtype, softmax):
-    q, k, v, do = rand_inputs(2, 2, 150, 64, dtype, cuda_device, std=1.0 if softmax else 0.5, seed=3)
-    compare_case(q, k, v, do, softmax=softmax, tag=f"{dtype}")
+def test_dtypes(cuda_device, dtype, softmax, D):
+    q, k, v, do = rand_inputs(2, 2, 150, D, dtype, cuda_device, std=1.0 if softmax else 0.5, seed=3)
+    compare_case(q, k, v, do, softmax=softmax, tag=f"{dtype} D{D}")
 
 
 @pytest.mark.parametrize("causal,num_prefix", [(False, 0), (True, 4), (True, 40), (True, 300)])
@@ -207,6 +208,21 @@ def test_masks(cuda_device, causal, num_prefix, softmax):
 def test_heavy_tailed_keys(cuda_device, D):
     q, k, v, do = rand_inputs(2, 4, 300, D, torch.bfloat16, cuda_device, seed=11, key_scale=0.5)
     compare_case(q, k, v, do, gamma=1.0 / (2 * math.sqrt(D)), tag=f"lognormal D{D}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("shift", [3.9, 6.0])
+def test_queries_far_from_every_key(cuda_device, dtype, shift):
+    """Queries of the first 90 tokens of every other head moved far from all
+    keys, so that even their nearest key sits ~100 (shift 3.9) or ~220
+    (shift 6) powers of two below the forward's static logit bound
+    c*0.5*||q||^2.  The first case stays on the static offset with row sums
+    near 2^-40; the second drops below 2^-60 and makes those work-groups
+    recompute with an online max."""
+    q, k, v, do = rand_inputs(2, 4, 200, 64, dtype, cuda_device, seed=17)
+    q = q.clone()
+    q[:, ::2, :90] += shift
+    compare_case(q, k, v, do, gamma=0.0625, tag=f"far{shift} {dtype}")
 
 
 def test_strided_views_like_the_model(cuda_device):
