@@ -160,14 +160,15 @@ __device__ inline int swap23(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 
 // Row of accumulator element i held by lane half h (32x32 MFMA C layout).
 __device__ inline int crow(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
 
-// Transposed operand fragment from a ROW-major 16-bit LDS tile X[token][feature]
-// with row stride LD elements (gfx950 ds_read_b64_tr_b16, two reads): lane
-// (m = lane % 32, h = lane / 32) receives feature fbase + m of the 8 tokens
-// tbase + 8(s/4) + 4h + s%4, s = 0..7 -- the contraction order of a P / dS
-// accumulator reused as the other operand (crow(8t + s, h) with tbase = 16t).
-// Within each 16-lane group, lane g addresses token row R0 + g/4 at feature
-// column n0 + 4(g%4) and receives X[R0 + e][n0 + g] for e = 0..3.
+// gfx950 ds_read_b64_tr_b16: within each 16-lane group, lane g addresses
+// token row R0 + g/4 at feature column n0 + 4(g%4) and receives
+// X[R0 + e][n0 + g] for e = 0..3.  Two such reads give lane (m = lane % 32,
+// h = lane / 32) feature fbase + m of the 8 tokens tbase + 8(s/4) + 4h + s%4,
+// s = 0..7 -- the contraction order of a P / dS accumulator reused as the
+// other MFMA operand (crow(8t + s, h) with tbase = 16t).  See ld_trc.
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+// Transposing read from a padded row-major tile (row stride LD elements).
 template <typename T, int LD>
 __device__ inline typename Elem<T>::frag ld_tr8(const T* tile, int tbase, int fbase, int lane) {
   static_assert(sizeof(T) == 2, "transposing LDS reads are for 16-bit elements");
@@ -370,6 +371,149 @@ struct Tile {
   }
 };
 
+// ---------------------------------------------------------------------------
+// Chunk-major LDS tile for 16-bit elements (ROWS tokens x DP features).  A
+// chunk is 8 consecutive features of one token (16 bytes).  The tile is
+// DP/8 chunk columns; column c holds chunk c of the ROWS tokens back to back
+// and is followed by 64 bytes of padding, so consecutive columns start 64
+// bytes apart modulo the 256 bytes that the 64 LDS banks cover.  Every access
+// pattern of the kernels is then free of bank conflicts:
+//   * row reads (ld8): 16 lanes read one chunk of 16 consecutive tokens --
+//     256 contiguous bytes;
+//   * transposing reads (ld_trc): 32 lanes read 4 chunks x 4 tokens -- four
+//     64-byte runs in four different bank quarters;
+//   * tile stores (CTile::store): 16 lanes write 4 chunks x 4 tokens, same.
+// Addresses are a per-lane base plus compile-time offsets.
+// ---------------------------------------------------------------------------
+template <int ROWS>
+struct CLayout {
+  static_assert(ROWS % 16 == 0, "chunk columns must span a multiple of 256 bytes");
+  static constexpr int CS = ROWS * 8 + 32;  // elements per chunk column
+  template <int DP>
+  static constexpr int size() { return DP / 8 * CS; }
+  __device__ static inline int off(int row, int col) { return (col >> 3) * CS + row * 8 + (col & 7); }
+};
+
+// Transposing read from a chunk-major tile: 8 consecutive tokens (in the
+// P / dS contraction order tbase + 8(s/4) + 4h + s%4) of feature fbase + n.
+template <typename T, int ROWS>
+__device__ inline typename Elem<T>::frag ld_trc(const T* tile, int tbase, int fbase, int lane) {
+  static_assert(sizeof(T) == 2, "transposing LDS reads are for 16-bit elements");
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+  const int g = lane & 15;
+  const int row = tbase + 4 * (lane >> 5) + (g >> 2);
+  const int col = fbase + 16 * ((lane >> 4) & 1) + 4 * (g & 3);
+  const T* a = tile + CLayout<ROWS>::off(row, col);
+  const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)a);
+  const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a + 64));  // row + 8
+  typedef short s16x8_t __attribute__((ext_vector_type(8)));
+  const s16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(typename Elem<T>::frag, v);
+}
+
+// Sum over lanes l and l ^ 16 (v_permlane16_swap).
+__device__ inline float xrow_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Cooperative chunk-major tile, staged global -> registers -> LDS.  Work
+// unit = one chunk.  Unit u maps to chunk 4*(u/16 mod DP/32) + u%4 of token
+// 4*(u/16 div DP/32) + (u/4)%4: 16 consecutive units cover 4 tokens x 4
+// chunks (64 contiguous bytes of each token in global memory).
+template <typename T, int ROWS, int DP, int NT>
+struct CTile {
+  typedef typename Elem<T>::frag frag;
+  typedef CLayout<ROWS> L;
+  static constexpr int CPR = DP / 8;
+  static constexpr int CG = CPR / 4;  // groups of 4 chunks per token
+  static constexpr int UNITS = ROWS * CPR;
+  static constexpr int PER = (UNITS + NT - 1) / NT;
+  static_assert(CPR % 4 == 0 && CG <= 4, "DP must be 32, 64 or 128");
+  frag r[PER];
+  int tok0_, n_;
+
+  __device__ static inline void unit(int u, int& row, int& ch) {
+    const int rest = u >> 4;
+    ch = 4 * (rest % CG) + (u & 3);
+    row = 4 * (rest / CG) + ((u >> 2) & 3);
+  }
+
+  __device__ inline void load(const T* base, int64_t sn, int tok0, int N, int D, int tid) {
+    tok0_ = tok0;
+    n_ = N;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int u = tid + j * NT;
+      int row, ch;
+      unit(u, row, ch);
+      const int tok = tok0 + row;
+      r[j] = (u < UNITS && tok >= 0 && tok < N && ch * 8 < D) ? ld8<T>(base + (int64_t)tok * sn + ch * 8) : zero_frag<T>();
+    }
+  }
+
+  __device__ inline void store(T* lds, int tid) const {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int u = tid + j * NT;
+      if (UNITS % NT != 0 && u >= UNITS) continue;
+      int row, ch;
+      unit(u, row, ch);
+      st8<T>(lds + L::off(row, 8 * ch), r[j]);
+    }
+  }
+
+  // nrm[row] = -0.5 * ||row||^2 in fp32 (from the input-dtype values), and
+  // -inf for padding rows (tokens outside [0, N)): used as the initial value
+  // of an S accumulator, it makes every logit against a padding key -inf, so
+  // padding needs no element mask.  A token's chunks sit in lanes that differ
+  // in lane bits 0-1 and, for DP > 32, 4-5.
+  __device__ inline void store_neg_halfnorm(float* nrm, int tid) const {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int u = tid + j * NT;
+      int row, ch;
+      unit(u, row, ch);
+      float s = group_sum<4>(sumsq8<T>(r[j]));
+      if constexpr (CG >= 2) s = xrow_sum(s);
+      if constexpr (CG >= 4) s = xhalf_sum(s);
+      const int tok = tok0_ + row;
+      if (ch == 0 && u < UNITS) nrm[row] = (tok >= 0 && tok < n_) ? -0.5f * s : -__builtin_inff();
+    }
+  }
+};
+
+// LDS tile layout of the kernels.  16-bit tiles with 128 features are
+// chunk-major (CLayout); narrower 16-bit tiles and fp32 tiles are row-major
+// with a 16-byte row pad, which measured faster for them (their row reads
+// and transposing reads are already nearly conflict-free).
+template <typename T, int DP>
+constexpr bool kChunkMajor = sizeof(T) == 2 && DP == 128;
+
+template <typename T, int ROWS, int DP, int NT>
+using TileFor = std::conditional_t<kChunkMajor<T, DP>, CTile<T, ROWS, DP, NT>, Tile<T, ROWS, DP, NT>>;
+
+template <typename T, int ROWS, int DP>
+struct TileLayout {
+  static constexpr bool CM = kChunkMajor<T, DP>;
+  static constexpr int LDR = DP + Elem<T>::PAD;
+  static constexpr int SIZE = CM ? CLayout<ROWS>::template size<DP>() : ROWS * LDR;
+  __device__ static inline int off(int row, int col) {
+    if constexpr (CM) return CLayout<ROWS>::off(row, col);
+    else return row * LDR + col;
+  }
+  template <typename TT>
+  __device__ static inline void store(const TT& tile, T* lds, int tid) {
+    if constexpr (CM) tile.store(lds, tid);
+    else tile.template store_rows<LDR>(lds, tid);
+  }
+  // V^T / K^T / Q^T / dO^T fragment (16-bit types)
+  __device__ static inline typename Elem<T>::frag tr(const T* tile, int tbase, int fbase, int lane) {
+    if constexpr (CM) return ld_trc<T, ROWS>(tile, tbase, fbase, lane);
+    else return ld_tr8<T, LDR>(tile, tbase, fbase, lane);
+  }
+};
+
 // Work-group -> (b*H + h, group) with an XCD-aware remap: the hardware deals
 // work-groups round-robin over the 8 XCDs, so consecutive logical indices
 // (the groups of one head, which share K/V or Q/dO) are packed onto the same
@@ -490,11 +634,15 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   typedef typename E::frag frag;
   constexpr int NT = 64 * W, KB = BN / 32, KS = DP / 16, ND = DP / 32;
   constexpr int LDR = DP + E::PAD, LDT = BN + E::PAD;
-  // 16-bit types keep V row-major and read V^T with transposing LDS reads;
-  // fp32 stages a transposed copy.
+  // 16-bit types keep K and V in chunk-major tiles and read V^T with
+  // transposing LDS reads; fp32 uses padded row-major K and a transposed copy
+  // of V.
   constexpr bool TR = sizeof(T) == 2;
-  __shared__ __attribute__((aligned(16))) T sK[2][BN * LDR];
-  __shared__ __attribute__((aligned(16))) T sVt[2][TR ? BN * LDR : DP * LDT];
+  typedef TileLayout<T, BN, DP> TLy;
+  constexpr int TSZ = TLy::SIZE;
+  __shared__ __attribute__((aligned(16))) T sK[2][TSZ];
+  __shared__ __attribute__((aligned(16))) T sVt[2][TR ? TSZ : DP * LDT];
+  auto roff = [](int row, int col) { return TLy::off(row, col); };
   __shared__ __attribute__((aligned(16))) float sKn[2][BN];
 
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
@@ -540,7 +688,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   f32x16_t oacc[ND], lacc;
   float m_run;
 
-  typedef Tile<T, BN, DP, NT> TileT;
+  typedef TileFor<T, BN, DP, NT> TileT;
   TileT tk, tv;
   auto load_kv = [&](int kt) {
     const int tok0 = org + 32 * (kt * KB - kshift);
@@ -558,10 +706,14 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
     load_kv(0);
     for (int kt = 0; kt < nkt; ++kt) {
       const int buf = kt & 1;
-      tk.template store_rows<LDR>(sK[buf], tid);
+      if constexpr (TR) {
+        TLy::store(tk, sK[buf], tid);
+        TLy::store(tv, sVt[buf], tid);
+      } else {
+        tk.template store_rows<LDR>(sK[buf], tid);
+        tv.template store_trans<LDT>(sVt[buf], tid);
+      }
       tk.store_neg_halfnorm(sKn[buf], tid);
-      if constexpr (TR) tv.template store_rows<LDR>(sVt[buf], tid);
-      else tv.template store_trans<LDT>(sVt[buf], tid);
       __syncthreads();
       if (kt + 1 < nkt) load_kv(kt + 1);
       if (!wave_on) continue;
@@ -572,7 +724,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
         if (!blk_any(q0, k0, causal, npre)) continue;
         frag kA[KS];
 #pragma unroll
-        for (int t = 0; t < KS; ++t) kA[t] = ld8<T>(sK[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h);
+        for (int t = 0; t < KS; ++t) kA[t] = ld8<T>(sK[buf] + roff(32 * kb + n, 16 * t + 8 * h));
         f32x16_t s = ld_rows16(sKn[buf] + 32 * kb, h);
 #pragma unroll
         for (int t = 0; t < KS; ++t) s = E::mma(kA[t], qf[t], s);
@@ -582,7 +734,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
         for (int d = 0; d < ND; ++d)
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            if constexpr (TR) vA[d][t] = ld_tr8<T, LDR>(sVt[buf], 32 * kb + 16 * t, 32 * d, lane);
+            if constexpr (TR) vA[d][t] = TLy::tr(sVt[buf], 32 * kb + 16 * t, 32 * d, lane);
             else vA[d][t] = ld8<T>(sVt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h));
           }
         if (!blk_nomask(q0, k0, causal, npre)) mask_key_rows(s, k0, h, jmax);
@@ -666,9 +818,12 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   // 16-bit types read K^T from the row-major K tile with transposing LDS
   // reads; fp32 stages a transposed copy.
   constexpr bool TR = sizeof(T) == 2;
-  __shared__ __attribute__((aligned(16))) T sK[2][BN * LDR];
+  typedef TileLayout<T, BN, DP> TLy;
+  constexpr int TSZ = TLy::SIZE;
+  __shared__ __attribute__((aligned(16))) T sK[2][TSZ];
   __shared__ __attribute__((aligned(16))) T sKt[TR ? 1 : 2][TR ? 8 : DP * LDT];
-  __shared__ __attribute__((aligned(16))) T sV[2][BN * LDR];
+  __shared__ __attribute__((aligned(16))) T sV[2][TSZ];
+  auto roff = [](int row, int col) { return TLy::off(row, col); };
   __shared__ __attribute__((aligned(16))) float sKn[2][BN];
 
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
@@ -748,7 +903,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
     rsum[j] = 0.f;
   }
 
-  Tile<T, BN, DP, NT> tk, tv;
+  TileFor<T, BN, DP, NT> tk, tv;
   {
     const int tok0 = org + 32 * (-kshift);
     tk.load(K, p.sk[2], tok0, N, D, tid);
@@ -756,10 +911,15 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   }
   for (int kt = 0; kt < nkt; ++kt) {
     const int buf = kt & 1;
-    tk.template store_rows<LDR>(sK[buf], tid);
-    if constexpr (!TR) tk.template store_trans<LDT>(sKt[buf], tid);
+    if constexpr (TR) {
+      TLy::store(tk, sK[buf], tid);
+      TLy::store(tv, sV[buf], tid);
+    } else {
+      tk.template store_rows<LDR>(sK[buf], tid);
+      tk.template store_trans<LDT>(sKt[buf], tid);
+      tv.template store_rows<LDR>(sV[buf], tid);
+    }
     tk.store_neg_halfnorm(sKn[buf], tid);
-    tv.template store_rows<LDR>(sV[buf], tid);
     __syncthreads();
     if (kt + 1 < nkt) {
       const int tok1 = org + 32 * ((kt + 1) * KB - kshift);
@@ -782,8 +942,8 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
       frag kA[KS], vA[KS];
 #pragma unroll
       for (int t = 0; t < KS; ++t) {
-        kA[t] = ld8<T>(sK[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h);
-        vA[t] = ld8<T>(sV[buf] + (32 * kb + n) * LDR + 16 * t + 8 * h);
+        kA[t] = ld8<T>(sK[buf] + roff(32 * kb + n, 16 * t + 8 * h));
+        vA[t] = ld8<T>(sV[buf] + roff(32 * kb + n, 16 * t + 8 * h));
       }
       const f32x16_t kinit = ld_rows16(sKn[buf] + 32 * kb, h);
       f32x16_t sacc[QPW], dpacc[QPW];
@@ -806,7 +966,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
         for (int d = 0; d < ND; ++d)
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            if constexpr (TR) ktA[d][t] = ld_tr8<T, LDR>(sK[buf], 32 * kb + 16 * t, 32 * d, lane);
+            if constexpr (TR) ktA[d][t] = TLy::tr(sK[buf], 32 * kb + 16 * t, 32 * d, lane);
             else ktA[d][t] = ld8<T>(sKt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h));
           }
       };
@@ -888,9 +1048,12 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   // 16-bit types read Q^T and dO^T from the row-major tiles with transposing
   // LDS reads; fp32 stages transposed copies.
   constexpr bool TR = sizeof(T) == 2;
-  __shared__ __attribute__((aligned(16))) T sQ[2][BM * LDR];
+  typedef TileLayout<T, BM, DP> TLy;
+  constexpr int TSZ = TLy::SIZE;
+  __shared__ __attribute__((aligned(16))) T sQ[2][TSZ];
   __shared__ __attribute__((aligned(16))) T sQt[TR ? 1 : 2][TR ? 8 : DP * LDT];
-  __shared__ __attribute__((aligned(16))) T sD[2][BM * LDR];
+  __shared__ __attribute__((aligned(16))) T sD[2][TSZ];
+  auto roff = [](int row, int col) { return TLy::off(row, col); };
   __shared__ __attribute__((aligned(16))) T sDt[TR ? 1 : 2][TR ? 8 : DP * LDT];
   __shared__ __attribute__((aligned(16))) float sOff[2][BM];
   __shared__ __attribute__((aligned(16))) float sDel[2][BM];
@@ -960,7 +1123,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   const int qshift = nqt_all * QB - nblk;
   const int qt_lo = (((qlo - org) >> 5) + qshift) / QB;
 
-  Tile<T, BM, DP, NT> tq, td;
+  TileFor<T, BM, DP, NT> tq, td;
   float offr = 0.f, delr = 0.f;
   auto load_tile = [&](int qt) {
     const int tok0 = org + 32 * (qt * QB - qshift);
@@ -976,9 +1139,12 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   load_tile(qt_lo);
   for (int qt = qt_lo; qt < nqt_all; ++qt) {
     const int buf = qt & 1;
-    tq.template store_rows<LDR>(sQ[buf], tid);
-    td.template store_rows<LDR>(sD[buf], tid);
-    if constexpr (!TR) {
+    if constexpr (TR) {
+      TLy::store(tq, sQ[buf], tid);
+      TLy::store(td, sD[buf], tid);
+    } else {
+      tq.template store_rows<LDR>(sQ[buf], tid);
+      td.template store_rows<LDR>(sD[buf], tid);
       tq.template store_trans<LDT>(sQt[buf], tid);
       td.template store_trans<LDT>(sDt[buf], tid);
     }
@@ -1011,8 +1177,8 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
           else dpacc[qb] = zero16();
 #pragma unroll
           for (int t = 0; t < KS; ++t) {
-            const frag qA = ld8<T>(sQ[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h);
-            const frag dA = ld8<T>(sD[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h);
+            const frag qA = ld8<T>(sQ[buf] + roff(32 * qb + n, 16 * t + 8 * h));
+            const frag dA = ld8<T>(sD[buf] + roff(32 * qb + n, 16 * t + 8 * h));
             sacc[qb] = E::mma(qA, kf[0][t], sacc[qb]);
             dpacc[qb] = E::mma(dA, vf[0][t], dpacc[qb]);
           }
@@ -1035,8 +1201,8 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
             for (int t = 0; t < 2; ++t) {
               frag dtA, qtA;
               if constexpr (TR) {
-                dtA = ld_tr8<T, LDR>(sD[buf], 32 * qb + 16 * t, 32 * d, lane);
-                qtA = ld_tr8<T, LDR>(sQ[buf], 32 * qb + 16 * t, 32 * d, lane);
+                dtA = TLy::tr(sD[buf], 32 * qb + 16 * t, 32 * d, lane);
+                qtA = TLy::tr(sQ[buf], 32 * qb + 16 * t, 32 * d, lane);
               } else {
                 const int o = (32 * d + n) * LDT + tchunk<BM>(32 * d + n, 32 * qb + 16 * t + 8 * h);
                 dtA = ld8<T>(sDt[buf] + o);
@@ -1063,8 +1229,8 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
       frag qA[KS], dA[KS];
 #pragma unroll
       for (int t = 0; t < KS; ++t) {
-        qA[t] = ld8<T>(sQ[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h);
-        dA[t] = ld8<T>(sD[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h);
+        qA[t] = ld8<T>(sQ[buf] + roff(32 * qb + n, 16 * t + 8 * h));
+        dA[t] = ld8<T>(sD[buf] + roff(32 * qb + n, 16 * t + 8 * h));
       }
       const f32x16_t oinit = ld_rows16(sOff[buf] + 32 * qb, h);
       f32x16_t dinit;
@@ -1093,8 +1259,8 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
             if constexpr (TR) {
-              dtA[d][t] = ld_tr8<T, LDR>(sD[buf], 32 * qb + 16 * t, 32 * d, lane);
-              qtA[d][t] = ld_tr8<T, LDR>(sQ[buf], 32 * qb + 16 * t, 32 * d, lane);
+              dtA[d][t] = TLy::tr(sD[buf], 32 * qb + 16 * t, 32 * d, lane);
+              qtA[d][t] = TLy::tr(sQ[buf], 32 * qb + 16 * t, 32 * d, lane);
             } else {
               const int o = (32 * d + n) * LDT + tchunk<BM>(32 * d + n, 32 * qb + 16 * t + 8 * h);
               dtA[d][t] = ld8<T>(sDt[buf] + o);
@@ -1187,9 +1353,9 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
   typedef typename E::frag frag;
   static_assert(sizeof(T) == 2, "the paired kernel reads transposed operands with ds_read_b64_tr_b16");
   constexpr int W = 2 * NP, NT = 64 * W, QB = BM / 32, KS = DP / 16, ND = DP / 32;
-  constexpr int LDR = DP + E::PAD;
-  __shared__ __attribute__((aligned(16))) T sQ[2][BM * LDR];
-  __shared__ __attribute__((aligned(16))) T sD[2][BM * LDR];
+  typedef TileLayout<T, BM, DP> TLy;
+  __shared__ __attribute__((aligned(16))) T sQ[2][TLy::SIZE];
+  __shared__ __attribute__((aligned(16))) T sD[2][TLy::SIZE];
   __shared__ __attribute__((aligned(16))) float sOff[2][BM];
   __shared__ __attribute__((aligned(16))) float sDel[2][BM];
   __shared__ __attribute__((aligned(16))) T sP[NP][QB][2 * 64 * 8];
@@ -1247,7 +1413,7 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
   const int qshift = nqt_all * QB - nblk;
   const int qt_lo = (((qlo - org) >> 5) + qshift) / QB;
 
-  Tile<T, BM, DP, NT> tq, td;
+  TileFor<T, BM, DP, NT> tq, td;
   float offr = 0.f, delr = 0.f;
   auto load_tile = [&](int qt) {
     const int tok0 = org + 32 * (qt * QB - qshift);
@@ -1268,8 +1434,8 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
     load_tile(qt_lo);
     for (int qt = qt_lo; qt < nqt_all; ++qt) {
       const int buf = qt & 1;
-      tq.template store_rows<LDR>(sQ[buf], tid);
-      td.template store_rows<LDR>(sD[buf], tid);
+      TLy::store(tq, sQ[buf], tid);
+      TLy::store(td, sD[buf], tid);
       if (tid < BM) {
         sOff[buf][tid] = offr;
         sDel[buf][tid] = delr;
@@ -1289,7 +1455,7 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
           const int q0 = org + 32 * (qblk0 + qb);
           f32x16_t s = ld_rows16(sOff[buf] + 32 * qb, h);
 #pragma unroll
-          for (int t = 0; t < KS; ++t) s = E::mma(ld8<T>(sQ[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h), kv[t], s);
+          for (int t = 0; t < KS; ++t) s = E::mma(ld8<T>(sQ[buf] + TLy::off(32 * qb + n, 16 * t + 8 * h)), kv[t], s);
           if (!blk_nomask(q0, k0, causal, npre)) mask_query_rows(s, q0, h, ilo);
 #pragma unroll
           for (int i = 0; i < 16; ++i) pf[qb][i >> 3][i & 7] = (T)fast_exp2(fmaf(s[i], c, nckn));
@@ -1305,7 +1471,7 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
           for (int d = 0; d < ND; ++d)
 #pragma unroll
             for (int t = 0; t < 2; ++t)
-              acc[d] = E::mma(ld_tr8<T, LDR>(sD[buf], 32 * qb + 16 * t, 32 * d, lane), pf[qb][t], acc[d]);
+              acc[d] = E::mma(TLy::tr(sD[buf], 32 * qb + 16 * t, 32 * d, lane), pf[qb][t], acc[d]);
         }
       } else {
         // phase 1: dP
@@ -1317,7 +1483,7 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
           if constexpr (SOFTMAX) dp = ld_rows16(sDel[buf] + 32 * qb, h);
           else dp = zero16();
 #pragma unroll
-          for (int t = 0; t < KS; ++t) dp = E::mma(ld8<T>(sD[buf] + (32 * qb + n) * LDR + 16 * t + 8 * h), kv[t], dp);
+          for (int t = 0; t < KS; ++t) dp = E::mma(ld8<T>(sD[buf] + TLy::off(32 * qb + n, 16 * t + 8 * h)), kv[t], dp);
           dpacc[qb] = dp;
         }
         __syncthreads();
@@ -1338,7 +1504,7 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
           for (int d = 0; d < ND; ++d)
 #pragma unroll
             for (int t = 0; t < 2; ++t)
-              acc[d] = E::mma(ld_tr8<T, LDR>(sQ[buf], 32 * qb + 16 * t, 32 * d, lane), sf[t], acc[d]);
+              acc[d] = E::mma(TLy::tr(sQ[buf], 32 * qb + 16 * t, 32 * d, lane), sf[t], acc[d]);
         }
       }
     }

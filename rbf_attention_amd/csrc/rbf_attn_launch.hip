@@ -42,8 +42,8 @@ hipError_t fwd_cfg(const Params& p, hipStream_t st) {
 
 template <int DP, bool SM, int W, int QPW, int BN, bool EARLY = true>
 hipError_t dq_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_bwd_dq_kernel<Elt, DP, W, QPW, BN, SM, EARLY>), dim3(grid_of(p, W * QPW)), dim3(64 * W), 0, st,
-                     p);
+  hipLaunchKernelGGL((rbf_bwd_dq_kernel<Elt, DP, W, QPW, BN, SM, EARLY>), dim3(grid_of(p, W * QPW)), dim3(64 * W), 0,
+                     st, p);
   return hipGetLastError();
 }
 
@@ -56,7 +56,8 @@ hipError_t dkdv_cfg(const Params& p, hipStream_t st) {
 
 template <int DP, bool SM, int NP, int BM>
 hipError_t dkdv_pair_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_bwd_dkdv_pair_kernel<Elt, DP, NP, BM, SM>), dim3(grid_of(p, NP)), dim3(128 * NP), 0, st, p);
+  hipLaunchKernelGGL((rbf_bwd_dkdv_pair_kernel<Elt, DP, NP, BM, SM>), dim3(grid_of(p, NP)), dim3(128 * NP), 0, st,
+                     p);
   return hipGetLastError();
 }
 
@@ -90,8 +91,10 @@ hipError_t dq_default(const Params& p, hipStream_t st) {
 template <int DP, bool SM>
 hipError_t dkdv_default(const Params& p, hipStream_t st) {
   if constexpr (kIsF32) return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
-  else if constexpr (DP <= 64) return dkdv_cfg<DP, SM, 4, 1, 128>(p, st);
-  else return dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
+  else if constexpr (DP <= 64)
+    return p.N >= kLongSeq ? dkdv_cfg<DP, SM, 8, 1, 128>(p, st) : dkdv_cfg<DP, SM, 4, 1, 128, false>(p, st);
+  else
+    return p.N >= kLongSeq ? dkdv_pair_cfg<DP, SM, 4, 64>(p, st) : dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
 }
 
 // ---- tuning candidates (bf16, 32 < D <= 64) ------------------------------
@@ -105,6 +108,7 @@ hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
     case 2: return fwd_cfg<DP, SM, 8, 64>(p, st);
     case 3: return fwd_cfg<DP, SM, 4, 128>(p, st);
     case 4: return fwd_cfg<DP, SM, 2, 64>(p, st);
+    case 5: return fwd_cfg<DP, SM, 4, 32>(p, st);
     default: break;
   }
 #endif
