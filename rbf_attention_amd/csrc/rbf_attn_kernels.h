@@ -1345,9 +1345,11 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
 //   phase 2  P-wave:  dV^T += dO^T P
 //            dS-wave: dS = P dP with P from LDS, dK^T += Q^T dS, colsum += dS
 // The dS-wave takes P as rounded to the element type, the precision at which
-// P also enters dV.
+// P also enters dV.  SGB: every 32-query block issues all of its LDS operand
+// reads before its MFMAs (sched_group_barrier), trading registers for hidden
+// LDS latency.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int NP, int BM, bool SOFTMAX>
+template <typename T, int DP, int NP, int BM, bool SOFTMAX, bool SGB = false>
 __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Params p) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -1456,6 +1458,10 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
           f32x16_t s = ld_rows16(sOff[buf] + 32 * qb, h);
 #pragma unroll
           for (int t = 0; t < KS; ++t) s = E::mma(ld8<T>(sQ[buf] + TLy::off(32 * qb + n, 16 * t + 8 * h)), kv[t], s);
+          if constexpr (SGB) {
+            __builtin_amdgcn_sched_group_barrier(0x100, KS + 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, KS, 0);
+          }
           if (!blk_nomask(q0, k0, causal, npre)) mask_query_rows(s, q0, h, ilo);
 #pragma unroll
           for (int i = 0; i < 16; ++i) pf[qb][i >> 3][i & 7] = (T)fast_exp2(fmaf(s[i], c, nckn));
@@ -1472,6 +1478,10 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
 #pragma unroll
             for (int t = 0; t < 2; ++t)
               acc[d] = E::mma(TLy::tr(sD[buf], 32 * qb + 16 * t, 32 * d, lane), pf[qb][t], acc[d]);
+          if constexpr (SGB) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 4 * ND, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * ND, 0);
+          }
         }
       } else {
         // phase 1: dP
@@ -1485,6 +1495,10 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
 #pragma unroll
           for (int t = 0; t < KS; ++t) dp = E::mma(ld8<T>(sD[buf] + TLy::off(32 * qb + n, 16 * t + 8 * h)), kv[t], dp);
           dpacc[qb] = dp;
+          if constexpr (SGB) {
+            __builtin_amdgcn_sched_group_barrier(0x100, KS + (SOFTMAX ? 4 : 0), 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, KS, 0);
+          }
         }
         __syncthreads();
         // phase 2: dS = P dP, dK^T += Q^T dS
@@ -1505,6 +1519,10 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
 #pragma unroll
             for (int t = 0; t < 2; ++t)
               acc[d] = E::mma(TLy::tr(sQ[buf], 32 * qb + 16 * t, 32 * d, lane), sf[t], acc[d]);
+          if constexpr (SGB) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 4 * ND, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * ND, 0);
+          }
         }
       }
     }

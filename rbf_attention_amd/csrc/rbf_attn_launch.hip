@@ -54,9 +54,9 @@ hipError_t dkdv_cfg(const Params& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int DP, bool SM, int NP, int BM>
+template <int DP, bool SM, int NP, int BM, bool SGB = false>
 hipError_t dkdv_pair_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_bwd_dkdv_pair_kernel<Elt, DP, NP, BM, SM>), dim3(grid_of(p, NP)), dim3(128 * NP), 0, st,
+  hipLaunchKernelGGL((rbf_bwd_dkdv_pair_kernel<Elt, DP, NP, BM, SM, SGB>), dim3(grid_of(p, NP)), dim3(128 * NP), 0, st,
                      p);
   return hipGetLastError();
 }
@@ -94,7 +94,7 @@ hipError_t dkdv_default(const Params& p, hipStream_t st) {
   else if constexpr (DP <= 64)
     return p.N >= kLongSeq ? dkdv_cfg<DP, SM, 8, 1, 128>(p, st) : dkdv_cfg<DP, SM, 4, 1, 128, false>(p, st);
   else
-    return p.N >= kLongSeq ? dkdv_pair_cfg<DP, SM, 4, 64>(p, st) : dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
+    return p.N >= kLongSeq ? dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st) : dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
 }
 
 // ---- tuning candidates (bf16, 32 < D <= 64) ------------------------------
@@ -160,6 +160,8 @@ hipError_t dkdv_any_cfg(const Params& p, hipStream_t st) {
       case 21: return dkdv_pair_cfg<DP, SM, 4, 32>(p, st);
       case 22: return dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
       case 23: return dkdv_pair_cfg<DP, SM, 2, 32>(p, st);
+      case 25: return dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st);
+      case 26: return dkdv_pair_cfg<DP, SM, 2, 64, true>(p, st);
       default: break;
     }
   }
