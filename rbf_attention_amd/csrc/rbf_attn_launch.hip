@@ -78,7 +78,7 @@ hipError_t fwd_default(const Params& p, hipStream_t st) {
   else if constexpr (DP <= 64)
     return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 128>(p, st) : fwd_cfg<DP, SM, 4, 64>(p, st);
   else
-    return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 64>(p, st) : fwd_cfg<DP, SM, 4, 64>(p, st);
+    return fwd_cfg<DP, SM, 8, 64>(p, st);
 }
 
 template <int DP, bool SM>
