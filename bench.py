@@ -156,6 +156,51 @@ def train_step_bench(dev, steps: int, warmup: int):
     }
 
 
+DECODE_WORKLOAD = {"B": 8, "H": 16, "T": 1, "L": 16384, "D": 128}
+
+
+def decode_bench(dev, iters: int):
+    """KV-cache decode (the build's rbf_attn_decode; no reference counterpart):
+    one new token per (batch, head) against a 16K-token bf16 cache.  HBM-bound:
+    the algorithmic bytes are the K and V caches plus q and o."""
+    import torch
+
+    from rbf_attention_amd import ops
+
+    c = DECODE_WORKLOAD
+    g = torch.Generator().manual_seed(7)
+    shape = (c["B"], c["H"], c["L"], c["D"])
+    k = torch.randn(shape, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(shape, generator=g).to(torch.bfloat16).to(dev)
+    q = torch.randn((c["B"], c["H"], c["T"], c["D"]), generator=g).to(torch.bfloat16).to(dev)
+    gamma = 1.0 / (2 * c["D"] ** 0.5)
+    for _ in range(3):
+        ops.rbf_decode(q, k, v, sm_scale=gamma)
+    stream = torch.cuda.current_stream(dev)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(iters):
+        ops.rbf_decode(q, k, v, sm_scale=gamma)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    nbytes = 2 * k.numel() * 2 + 2 * q.numel() * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "decode HBM GB/s",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "us_per_call": round(ms * 1e3, 2),
+        "iters": iters,
+        "dtype": "bf16",
+        "config": dict(c, workload="decode_kv16k_bf16", softmax=True, gamma=gamma),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_GBS, 4), "traffic": None},
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -166,6 +211,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-train-step", action="store_true", help="skip the config-5 train-step measurement")
     ap.add_argument("--train-steps", type=int, default=20)
+    ap.add_argument("--no-decode", action="store_true", help="skip the KV-cache decode measurement")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="run one device copy of this many MiB before timing (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -290,6 +336,10 @@ def main() -> int:
         log("train step (config 5) ...")
         result["train_step"] = train_step_bench(dev, args.train_steps, 3)
         log(f"  {result['train_step']['value']} tokens/s, {result['train_step']['ms_per_step']} ms/step")
+    if not args.no_decode:
+        log("decode (KV cache) ...")
+        result["decode"] = decode_bench(dev, 50)
+        log(f"  {result['decode']['value']} GB/s, {result['decode']['us_per_call']} us/call")
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)

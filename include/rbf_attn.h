@@ -120,6 +120,44 @@ int rbf_attn_bwd(const rbf_attn_args* args, void* stream);
  */
 int rbf_attn_bwd_stage(const rbf_attn_args* args, void* stream, int stage);
 
+/*
+ * Decode against a KV cache: T new query tokens per (batch, head) attend to
+ * the cached keys and values.  No reference counterpart -- the reference has
+ * no decode path (its README lists one as future work); this is the
+ * "KV-cache decode" next step of the build.  Query t of batch b sits at
+ * cache position len_b - T + t and sees keys [0, len_b - T + t]: the cache
+ * already holds the new tokens' K and V.  The key axis is split over
+ * work-groups; partial results go to a caller-provided fp32 workspace and a
+ * second kernel merges them (softmax: log-sum-exp weights; non-softmax: sum).
+ */
+typedef struct rbf_attn_decode_args {
+  int32_t abi_version; /* must be RBF_ATTN_ABI_VERSION                       */
+  int32_t variant;     /* RBF_ATTN_SOFTMAX | RBF_ATTN_NON_SOFTMAX            */
+  int32_t dtype;       /* element type of q, k, v, o                         */
+  int32_t B, H;
+  int32_t T;           /* new query tokens per (b, h): 1 <= T <= 32          */
+  int32_t D;           /* 8 <= D <= 128, D % 8 == 0                          */
+  int32_t L;           /* cache length (maximum over the batch), L >= T      */
+  float gamma;         /* RBF bandwidth                                      */
+  rbf_attn_tensor q;   /* (B, H, T, D)                                        */
+  rbf_attn_tensor k, v; /* (B, H, >= L, D) caches                             */
+  rbf_attn_tensor o;   /* (B, H, T, D), written                              */
+  const int32_t* lens; /* optional device int32[B]: per-batch cache lengths,
+                          each in [T, L]; NULL = every batch entry has L     */
+  float* lse;          /* optional (softmax): fp32 contiguous (B, H, T) base-2
+                          log-sum-exp, written; NULL = not written           */
+  void* workspace;     /* fp32 scratch, rbf_attn_decode_workspace_size bytes,
+                          16-byte aligned, overwritten                       */
+  uint64_t workspace_bytes;
+} rbf_attn_decode_args;
+
+/* Bytes of workspace rbf_attn_decode needs for these sizes (0 on invalid
+ * sizes; the reason is in rbf_attn_last_error). */
+uint64_t rbf_attn_decode_workspace_size(const rbf_attn_decode_args* args);
+
+/* Decode: writes o (and lse when given).  Two launches on the stream. */
+int rbf_attn_decode(const rbf_attn_decode_args* args, void* stream);
+
 /* Message describing the last failed call on this thread ("" if none).
  * No reference counterpart: the reference surfaces Triton exceptions. */
 const char* rbf_attn_last_error(void);

@@ -15,6 +15,9 @@ It restates, in numpy float64, the reference's PyTorch math paths:
               fused kernel stores it                  rbf_attention.py:191-219
 * non-softmax exp(masked logits) @ V                  rbf_attention.py:1747-1753
               ("rbf_non_softmax_slow")
+* decode      the last T query rows of the causal forward over a KV cache
+              (no reference counterpart; pinned to softmax_forward /
+              non_softmax_forward)
 * augmented   q' = [q, 1, 0...], k' = [k, -||k||^2/2, 0...] padded to a
               multiple of 8, SDPA with scale 2*gamma  test_equivalence.py:9-33,
               rbf_math_test.py:46-64, rbf_attention.py:1718-1735
@@ -147,6 +150,38 @@ def non_softmax_backward(q, k, v, dO, gamma: float, causal: bool = True, num_pre
         dQ[b, h] = 2.0 * gamma * (dS @ ks - dS.sum(axis=1)[:, None] * qs)
         dK[b, h] = 2.0 * gamma * (dS.T @ qs - dS.sum(axis=0)[:, None] * ks)
     return dQ, dK, dV
+
+
+def decode_forward(q, k, v, gamma: float, softmax: bool = True, lens=None):
+    """KV-cache decode: q (B,H,T,D) against caches k, v (B,H,L,D).  Query t of
+    batch b sits at position lens[b] - T + t (lens defaults to L) and sees
+    keys [0, that position]: rows lens[b]-T .. lens[b]-1 of the causal forward
+    over the first lens[b] cached tokens (the reference has no decode path;
+    this is its causal attention restricted to the last T query rows, with
+    rbf_attention.py:1547-1553 logits).  Returns (O, L) in float64; L is the
+    base-2 LSE as in softmax_forward, and None for the non-softmax variant."""
+    q, k, v = _f64(q), _f64(k), _f64(v)
+    B, H, T, D = q.shape
+    Lc = k.shape[2]
+    lens = [Lc] * B if lens is None else [int(x) for x in lens]
+    O = np.zeros_like(q)
+    Lse = np.empty((B, H, T))
+    for b in range(B):
+        n = lens[b]
+        pos = np.arange(n - T, n)[:, None]
+        mask = np.arange(n)[None, :] <= pos
+        for h in range(H):
+            s = rbf_logits(q[b, h], k[b, h, :n], gamma)
+            s = np.where(mask, s, -np.inf)
+            if softmax:
+                m = s.max(axis=-1, keepdims=True)
+                e = np.exp(s - m)
+                l = e.sum(axis=-1, keepdims=True)
+                O[b, h] = (e / l) @ v[b, h, :n]
+                Lse[b, h] = (m[:, 0] + np.log(l[:, 0]) + gamma * np.einsum("td,td->t", q[b, h], q[b, h])) * LOG2E
+            else:
+                O[b, h] = np.exp(s) @ v[b, h, :n]
+    return O, (Lse if softmax else None)
 
 
 def augment(q, k):

@@ -5,6 +5,7 @@ backward, as hand-written HIP kernels for gfx950 behind a C ABI
 from .ops import (  # noqa: F401
     TritonNonSoftmaxRBFAttention,
     TritonRBFAttention,
+    rbf_decode,
     rbf_non_softmax_bwd,
     rbf_non_softmax_fwd,
     rbf_scaled_bwd,
@@ -22,4 +23,5 @@ __all__ = [
     "rbf_scaled_bwd",
     "rbf_non_softmax_fwd",
     "rbf_non_softmax_bwd",
+    "rbf_decode",
 ]

@@ -33,7 +33,15 @@ ERRORS = {
 }
 
 # Every extern "C" entry point of include/rbf_attn.h.
-EXPORTS = ("rbf_attn_fwd", "rbf_attn_bwd", "rbf_attn_bwd_stage", "rbf_attn_last_error", "rbf_attn_abi_version")
+EXPORTS = (
+    "rbf_attn_fwd",
+    "rbf_attn_bwd",
+    "rbf_attn_bwd_stage",
+    "rbf_attn_decode_workspace_size",
+    "rbf_attn_decode",
+    "rbf_attn_last_error",
+    "rbf_attn_abi_version",
+)
 
 
 class Tensor(ctypes.Structure):
@@ -67,6 +75,28 @@ class Args(ctypes.Structure):
         ("dv", Tensor),
         ("lse", ctypes.c_void_p),
         ("delta", ctypes.c_void_p),
+    ]
+
+
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("variant", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("B", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("D", ctypes.c_int32),
+        ("L", ctypes.c_int32),
+        ("gamma", ctypes.c_float),
+        ("q", Tensor),
+        ("k", Tensor),
+        ("v", Tensor),
+        ("o", Tensor),
+        ("lens", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_uint64),
     ]
 
 
@@ -116,6 +146,10 @@ def load(path: str | None = None):
         lib.rbf_attn_bwd.restype = ctypes.c_int
         lib.rbf_attn_bwd_stage.argtypes = [ctypes.POINTER(Args), ctypes.c_void_p, ctypes.c_int]
         lib.rbf_attn_bwd_stage.restype = ctypes.c_int
+        lib.rbf_attn_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs)]
+        lib.rbf_attn_decode_workspace_size.restype = ctypes.c_uint64
+        lib.rbf_attn_decode.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]
+        lib.rbf_attn_decode.restype = ctypes.c_int
         lib.rbf_attn_last_error.argtypes = []
         lib.rbf_attn_last_error.restype = ctypes.c_char_p
         lib.rbf_attn_abi_version.argtypes = []
@@ -137,7 +171,15 @@ def tensor_desc(t: torch.Tensor | None) -> Tensor:
     return Tensor(t.data_ptr(), s[0], s[1], s[2])
 
 
-def call(fn_name: str, args: Args, stream: int, *extra: int) -> None:
+def decode_workspace_size(args: DecodeArgs) -> int:
+    lib = load()
+    n = lib.rbf_attn_decode_workspace_size(ctypes.byref(args))
+    if n == 0:
+        raise RbfAttnError(-1, lib.rbf_attn_last_error().decode(errors="replace"))
+    return int(n)
+
+
+def call(fn_name: str, args, stream: int, *extra: int) -> None:
     lib = load()
     rc = getattr(lib, fn_name)(ctypes.byref(args), ctypes.c_void_p(stream), *extra)
     if rc != 0:

@@ -11,6 +11,7 @@
 #include "rbf_attn.h"
 #include "rbf_attn_kernels.h"
 #include "rbf_attn_launch.h"
+#include "rbf_decode_kernels.h"
 
 namespace {
 
@@ -115,9 +116,109 @@ int launched(hipError_t e, const char* what) {
   return RBF_ATTN_OK;
 }
 
+// Decode: validation and split geometry (shared by the workspace query and
+// the launch, so both agree on the workspace size).
+struct DecodeGeom {
+  int dp, waves, nsplit, tps;
+  uint64_t ws_bytes;
+};
+
+int decode_check(const rbf_attn_decode_args* a, DecodeGeom* g) {
+  g_err[0] = '\0';
+  if (a == nullptr) return fail(RBF_ATTN_EINVAL_ARGS, "args is NULL");
+  if (a->abi_version != RBF_ATTN_ABI_VERSION)
+    return fail(RBF_ATTN_EINVAL_ARGS, "abi_version %d != library %d", a->abi_version, RBF_ATTN_ABI_VERSION);
+  if (a->variant != RBF_ATTN_SOFTMAX && a->variant != RBF_ATTN_NON_SOFTMAX)
+    return fail(RBF_ATTN_EINVAL_ARGS, "unknown variant %d", a->variant);
+  if (a->dtype != RBF_ATTN_BF16 && a->dtype != RBF_ATTN_FP16 && a->dtype != RBF_ATTN_FP32)
+    return fail(RBF_ATTN_EINVAL_DTYPE, "unknown dtype %d", a->dtype);
+  if (a->B < 0 || a->H < 0) return fail(RBF_ATTN_EINVAL_SHAPE, "negative size B=%d H=%d", a->B, a->H);
+  if (a->T < 1 || a->T > 32) return fail(RBF_ATTN_EINVAL_SHAPE, "T=%d query tokens unsupported (need 1..32)", a->T);
+  if (a->L < a->T || a->L > (1 << 30)) return fail(RBF_ATTN_EINVAL_SHAPE, "cache length L=%d must be in [T, 2^30]", a->L);
+  if (a->D < 8 || a->D > 128 || a->D % 8 != 0)
+    return fail(RBF_ATTN_EINVAL_HEADDIM, "head dim D=%d unsupported (need 8 <= D <= 128, D %% 8 == 0)", a->D);
+  if (!(a->gamma > 0.f) || !isfinite(a->gamma))
+    return fail(RBF_ATTN_EINVAL_ARGS, "gamma must be finite and > 0 (got %g)", (double)a->gamma);
+  const long long bh = (long long)a->B * a->H;
+  if (bh > 0x7fffffffLL / 32) return fail(RBF_ATTN_EINVAL_SHAPE, "B*H=%lld too large", bh);
+  g->dp = a->D <= 32 ? 32 : a->D <= 64 ? 64 : 128;
+  // Split the key axis so that about 1024 work-groups run (4 per CU).
+  g->waves = rbf::decode_waves(a->dtype == RBF_ATTN_FP32);
+  const int tile = 32 * g->waves;
+  const int ntiles = (a->L + tile - 1) / tile;
+  long long ns = bh > 0 ? (1024 + bh - 1) / bh : 1;
+  if (ns > ntiles) ns = ntiles;
+  if (ns < 1) ns = 1;
+  g->tps = (int)((ntiles + ns - 1) / ns);
+  g->nsplit = (ntiles + g->tps - 1) / g->tps;
+  if (g->nsplit > 65535) return fail(RBF_ATTN_EINVAL_SHAPE, "too many key splits");
+  const long long P = (long long)g->nsplit * g->waves;
+  g->ws_bytes = (uint64_t)rbf::decode_ws_floats((int)bh, (int)P, a->T, g->dp) * 4;
+  return RBF_ATTN_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+uint64_t rbf_attn_decode_workspace_size(const rbf_attn_decode_args* a) {
+  DecodeGeom g;
+  if (decode_check(a, &g)) return 0;
+  return g.ws_bytes;
+}
+
+int rbf_attn_decode(const rbf_attn_decode_args* a, void* stream) {
+  DecodeGeom g;
+  int rc = decode_check(a, &g);
+  if (rc) return rc;
+  const size_t esz = elem_size(a->dtype);
+  if ((rc = check_tensor("q", a->q, esz))) return rc;
+  if ((rc = check_tensor("k", a->k, esz))) return rc;
+  if ((rc = check_tensor("v", a->v, esz))) return rc;
+  if ((rc = check_tensor("o", a->o, esz))) return rc;
+  if (a->lse != nullptr && reinterpret_cast<uintptr_t>(a->lse) % 4 != 0)
+    return fail(RBF_ATTN_EINVAL_STRIDE, "lse: not 4-byte aligned");
+  if (a->lens != nullptr && reinterpret_cast<uintptr_t>(a->lens) % 4 != 0)
+    return fail(RBF_ATTN_EINVAL_STRIDE, "lens: not 4-byte aligned");
+  if ((long long)a->B * a->H == 0) return RBF_ATTN_OK;
+  if (a->workspace == nullptr) return fail(RBF_ATTN_EINVAL_PTR, "workspace: null pointer");
+  if (reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0)
+    return fail(RBF_ATTN_EINVAL_STRIDE, "workspace: not 16-byte aligned");
+  if (a->workspace_bytes < g.ws_bytes)
+    return fail(RBF_ATTN_EINVAL_ARGS, "workspace of %llu bytes, %llu needed", (unsigned long long)a->workspace_bytes,
+                (unsigned long long)g.ws_bytes);
+  rbf::DecodeParams p = {};
+  p.q = a->q.ptr;
+  p.k = a->k.ptr;
+  p.v = a->v.ptr;
+  p.o = a->o.ptr;
+  copy_strides(p.sq, a->q);
+  copy_strides(p.sk, a->k);
+  copy_strides(p.sv, a->v);
+  copy_strides(p.so, a->o);
+  p.lens = a->lens;
+  p.lse = a->variant == RBF_ATTN_SOFTMAX ? a->lse : nullptr;
+  p.ws = reinterpret_cast<float*>(a->workspace);
+  p.B = a->B;
+  p.H = a->H;
+  p.T = a->T;
+  p.D = a->D;
+  p.L = a->L;
+  p.nsplit = g.nsplit;
+  p.tps = g.tps;
+  p.W = g.waves;
+  p.gamma = a->gamma;
+  p.c = (float)(2.0 * (double)a->gamma * 1.4426950408889634);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (a->dtype) {
+    case RBF_ATTN_BF16: e = rbf::launch_decode_bf16(p, a->variant, st); break;
+    case RBF_ATTN_FP16: e = rbf::launch_decode_fp16(p, a->variant, st); break;
+    default: e = rbf::launch_decode_fp32(p, a->variant, st); break;
+  }
+  return launched(e, "decode");
+}
+
 
 int rbf_attn_abi_version(void) { return RBF_ATTN_ABI_VERSION; }
 

@@ -7,17 +7,23 @@
 namespace rbf {
 
 struct Params;
+struct DecodeParams;
 
 // variant: 0 = softmax, 1 = non-softmax.  Return the launch status.
 #define RBF_DECLARE_LAUNCHERS(NAME)                                              \
   hipError_t launch_fwd_##NAME(const Params& p, int variant, hipStream_t st);   \
   hipError_t launch_bwd_dq_##NAME(const Params& p, int variant, hipStream_t st); \
-  hipError_t launch_bwd_dkdv_##NAME(const Params& p, int variant, hipStream_t st);
+  hipError_t launch_bwd_dkdv_##NAME(const Params& p, int variant, hipStream_t st); \
+  hipError_t launch_decode_##NAME(const DecodeParams& p, int variant, hipStream_t st);
 
 RBF_DECLARE_LAUNCHERS(bf16)
 RBF_DECLARE_LAUNCHERS(fp16)
 RBF_DECLARE_LAUNCHERS(fp32)
 
 #undef RBF_DECLARE_LAUNCHERS
+
+// Decode split geometry: waves per work-group (one 32-key block each per
+// tile); fp32 tiles need twice the LDS, so fp32 runs half as many.
+inline int decode_waves(int dtype_is_fp32) { return dtype_is_fp32 ? 2 : 4; }
 
 }  // namespace rbf

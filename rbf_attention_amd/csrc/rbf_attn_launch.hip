@@ -11,6 +11,7 @@
 
 #include "rbf_attn_kernels.h"
 #include "rbf_attn_launch.h"
+#include "rbf_decode_kernels.h"
 
 #ifndef RBF_ELEM_ID
 #error "RBF_ELEM_ID must be defined (0 bf16, 1 fp16, 2 fp32)"
@@ -209,6 +210,24 @@ hipError_t dkdv_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH
 
 #undef RBF_DISPATCH
 
+template <int DP, bool SM>
+hipError_t decode_dp(const DecodeParams& p, hipStream_t st) {
+  constexpr int W = kIsF32 ? 2 : 4;
+  if (p.W != W) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((rbf_decode_split_kernel<Elt, DP, W, SM>), dim3(p.B * p.H, p.nsplit), dim3(64 * W), 0, st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((rbf_decode_merge_kernel<Elt, DP, SM>), dim3(p.B * p.H * p.T), dim3(64), 0, st, p);
+  return hipGetLastError();
+}
+
+hipError_t decode_any(const DecodeParams& p, int variant, hipStream_t st) {
+  const bool sm = variant == 0;
+  if (p.D <= 32) return sm ? decode_dp<32, true>(p, st) : decode_dp<32, false>(p, st);
+  if (p.D <= 64) return sm ? decode_dp<64, true>(p, st) : decode_dp<64, false>(p, st);
+  return sm ? decode_dp<128, true>(p, st) : decode_dp<128, false>(p, st);
+}
+
 }  // namespace
 
 #if RBF_ELEM_ID == 0
@@ -229,6 +248,9 @@ hipError_t RBF_CAT(launch_bwd_dq_, RBF_NAME)(const Params& p, int variant, hipSt
 }
 hipError_t RBF_CAT(launch_bwd_dkdv_, RBF_NAME)(const Params& p, int variant, hipStream_t st) {
   return dkdv_any(p, variant, st);
+}
+hipError_t RBF_CAT(launch_decode_, RBF_NAME)(const DecodeParams& p, int variant, hipStream_t st) {
+  return decode_any(p, variant, st);
 }
 
 }  // namespace rbf

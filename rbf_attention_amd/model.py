@@ -92,7 +92,8 @@ class RBFAttention(nn.Module):
             pos = self.position_embedding(s, q.dtype)
             q, k = q + pos, k + pos
         fn = ops.run_triton_rbf if self.attention_type == "rbf" else ops.run_triton_non_softmax_rbf
-        out = fn(q, k, v, True, sm_scale=self.sm_scale, num_prefix=self.num_prefix)
+        # token-major output: the transpose + reshape below is then a view
+        out = fn(q, k, v, True, sm_scale=self.sm_scale, num_prefix=self.num_prefix, token_major=not self.apply_xsa)
         if self.apply_xsa:
             v_n = F.normalize(v, dim=-1)
             out = out - (out * v_n).sum(dim=-1, keepdim=True) * v_n

@@ -108,12 +108,22 @@ def _unpad(t: torch.Tensor, d: int) -> torch.Tensor:
 # ---------------------------------------------------------------------------
 # Implementations (shared by the reference-schema ops and the _ex ops)
 # ---------------------------------------------------------------------------
-def _softmax_fwd(q, k, v, is_causal: bool, sm_scale: float, num_prefix: int):
+def _alloc_out(q: torch.Tensor, dp: int, token_major: bool) -> torch.Tensor:
+    """(B, H, N, dp) output.  token_major: backed by a (B, N, H, dp) buffer, so
+    that ``out.transpose(1, 2).reshape(B, N, H * dp)`` -- the layout the model's
+    output projection reads (rbf_attention.py:1761) -- is a view, not a copy."""
+    B, H, N, _ = q.shape
+    if token_major:
+        return torch.empty((B, N, H, dp), device=q.device, dtype=q.dtype).transpose(1, 2)
+    return torch.empty((B, H, N, dp), device=q.device, dtype=q.dtype)
+
+
+def _softmax_fwd(q, k, v, is_causal: bool, sm_scale: float, num_prefix: int, token_major: bool = False):
     _check_inputs("scaled_fwd", q, k, v)
     B, H, N, D = q.shape
     dp = _padded_dim(D)
     q_, k_, v_ = _prep(q, dp), _prep(k, dp), _prep(v, dp)
-    out = torch.empty((B, H, N, dp), device=q.device, dtype=q.dtype)
+    out = _alloc_out(q, dp, token_major and dp == D)
     L = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
     a = _base_args(_lib.SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
     a.q, a.k, a.v, a.o = (_lib.tensor_desc(t) for t in (q_, k_, v_, out))
@@ -143,12 +153,12 @@ def _softmax_bwd(q, k, v, out, L, dout, is_causal: bool, sm_scale: float, num_pr
     return _unpad(dq, D), _unpad(dk, D), _unpad(dv, D)
 
 
-def _non_softmax_fwd(q, k, v, is_causal: bool, sm_scale: float, num_prefix: int):
+def _non_softmax_fwd(q, k, v, is_causal: bool, sm_scale: float, num_prefix: int, token_major: bool = False):
     _check_inputs("non_softmax_fwd", q, k, v)
     B, H, N, D = q.shape
     dp = _padded_dim(D)
     q_, k_, v_ = _prep(q, dp), _prep(k, dp), _prep(v, dp)
-    out = torch.empty((B, H, N, dp), device=q.device, dtype=q.dtype)
+    out = _alloc_out(q, dp, token_major and dp == D)
     a = _base_args(_lib.NON_SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
     a.q, a.k, a.v, a.o = (_lib.tensor_desc(t) for t in (q_, k_, v_, out))
     _launch("rbf_attn_fwd", a, q.device)
@@ -289,18 +299,29 @@ torch.library.register_autograd(
 # ---------------------------------------------------------------------------
 @torch.library.custom_op(f"{_EX}::scaled_fwd_ex", mutates_args=())
 def rbf_scaled_fwd_ex(
-    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, is_causal: bool, sm_scale: float, num_prefix: int
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    is_causal: bool,
+    sm_scale: float,
+    num_prefix: int,
+    token_major: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    return _softmax_fwd(q, k, v, is_causal, sm_scale, num_prefix)
+    return _softmax_fwd(q, k, v, is_causal, sm_scale, num_prefix, token_major)
+
+
+def _fake_out(q: torch.Tensor, token_major: bool) -> torch.Tensor:
+    dp = _padded_dim(q.shape[-1])
+    if token_major and dp == q.shape[-1]:
+        B, H, N, D = q.shape
+        return torch.empty((B, N, H, D), device=q.device, dtype=q.dtype).transpose(1, 2)
+    return torch.empty_like(q, memory_format=torch.contiguous_format)
 
 
 @rbf_scaled_fwd_ex.register_fake
-def _(q, k, v, is_causal, sm_scale, num_prefix):
+def _(q, k, v, is_causal, sm_scale, num_prefix, token_major=False):
     B, H, N, _ = q.shape
-    return (
-        torch.empty_like(q, memory_format=torch.contiguous_format),
-        torch.empty((B, H, N), device=q.device, dtype=torch.float32),
-    )
+    return _fake_out(q, token_major), torch.empty((B, H, N), device=q.device, dtype=torch.float32)
 
 
 @torch.library.custom_op(f"{_EX}::scaled_bwd_ex", mutates_args=())
@@ -324,7 +345,7 @@ def _(q, k, v, out, L, dout, is_causal, sm_scale, num_prefix):
 
 
 def _scaled_ex_setup_context(ctx, inputs, output):
-    q, k, v, is_causal, sm_scale, num_prefix = inputs
+    q, k, v, is_causal, sm_scale, num_prefix = inputs[:6]
     out, L = output
     ctx.save_for_backward(q, k, v, out, L)
     ctx.is_causal, ctx.sm_scale, ctx.num_prefix = is_causal, sm_scale, num_prefix
@@ -335,7 +356,7 @@ def _scaled_ex_backward(ctx, dout, dL):
     dq, dk, dv = torch.ops.rbf_attn_amd.scaled_bwd_ex(
         q, k, v, out, L, dout, ctx.is_causal, ctx.sm_scale, ctx.num_prefix
     )
-    return dq, dk, dv, None, None, None
+    return dq, dk, dv, None, None, None, None
 
 
 torch.library.register_autograd(f"{_EX}::scaled_fwd_ex", _scaled_ex_backward, setup_context=_scaled_ex_setup_context)
@@ -343,14 +364,20 @@ torch.library.register_autograd(f"{_EX}::scaled_fwd_ex", _scaled_ex_backward, se
 
 @torch.library.custom_op(f"{_EX}::non_softmax_fwd_ex", mutates_args=())
 def rbf_non_softmax_fwd_ex(
-    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, is_causal: bool, sm_scale: float, num_prefix: int
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    is_causal: bool,
+    sm_scale: float,
+    num_prefix: int,
+    token_major: bool = False,
 ) -> torch.Tensor:
-    return _non_softmax_fwd(q, k, v, is_causal, sm_scale, num_prefix)
+    return _non_softmax_fwd(q, k, v, is_causal, sm_scale, num_prefix, token_major)
 
 
 @rbf_non_softmax_fwd_ex.register_fake
-def _(q, k, v, is_causal, sm_scale, num_prefix):
-    return torch.empty_like(q, memory_format=torch.contiguous_format)
+def _(q, k, v, is_causal, sm_scale, num_prefix, token_major=False):
+    return _fake_out(q, token_major)
 
 
 @torch.library.custom_op(f"{_EX}::non_softmax_bwd_ex", mutates_args=())
@@ -372,7 +399,7 @@ def _(q, k, v, dout, is_causal, sm_scale, num_prefix):
 
 
 def _non_softmax_ex_setup_context(ctx, inputs, output):
-    q, k, v, is_causal, sm_scale, num_prefix = inputs
+    q, k, v, is_causal, sm_scale, num_prefix = inputs[:6]
     ctx.save_for_backward(q, k, v)
     ctx.is_causal, ctx.sm_scale, ctx.num_prefix = is_causal, sm_scale, num_prefix
 
@@ -382,7 +409,7 @@ def _non_softmax_ex_backward(ctx, dout):
     dq, dk, dv = torch.ops.rbf_attn_amd.non_softmax_bwd_ex(
         q, k, v, dout, ctx.is_causal, ctx.sm_scale, ctx.num_prefix
     )
-    return dq, dk, dv, None, None, None
+    return dq, dk, dv, None, None, None, None
 
 
 torch.library.register_autograd(
@@ -391,23 +418,108 @@ torch.library.register_autograd(
 
 
 # ---------------------------------------------------------------------------
+# KV-cache decode (no reference counterpart: the reference has no decode path)
+# ---------------------------------------------------------------------------
+def _decode(q, k_cache, v_cache, cache_lens, softmax: bool, sm_scale: float):
+    if q.dim() != 4 or k_cache.dim() != 4 or v_cache.dim() != 4:
+        raise ValueError("decode: q must be (B, H, T, D) and the caches (B, H, L, D)")
+    B, H, T, D = q.shape
+    if k_cache.shape != v_cache.shape or k_cache.shape[:2] != (B, H) or k_cache.shape[3] != D:
+        raise ValueError(f"decode: cache shapes {tuple(k_cache.shape)} / {tuple(v_cache.shape)} do not match q {tuple(q.shape)}")
+    for t in (k_cache, v_cache):
+        if t.dtype != q.dtype or t.device != q.device:
+            raise TypeError("decode: q and the caches must share dtype and device")
+    if q.dtype not in _lib.DTYPE_CODES:
+        raise TypeError(f"decode: unsupported dtype {q.dtype} (bf16, fp16, fp32)")
+    if q.device.type != "cuda":
+        raise RuntimeError("decode: the kernels run only on a ROCm GPU (there is no CPU fallback)")
+    if D > 128:
+        raise ValueError(f"decode: head dim {D} > 128 is not supported")
+    if not 1 <= T <= 32:
+        raise ValueError(f"decode: {T} query tokens per step unsupported (1..32)")
+    L = k_cache.shape[2]
+    if L < T:
+        raise ValueError(f"decode: cache length {L} < {T} query tokens")
+    dp = _padded_dim(D)
+    q_, k_, v_ = _prep(q, dp), _prep(k_cache, dp), _prep(v_cache, dp)
+    out = torch.empty((B, H, T, dp), device=q.device, dtype=q.dtype)
+    lse = torch.empty((B, H, T), device=q.device, dtype=torch.float32)
+    if B * H == 0:
+        return _unpad(out, D), lse
+    a = _lib.DecodeArgs()
+    a.abi_version = _lib.ABI_VERSION
+    a.variant = _lib.SOFTMAX if softmax else _lib.NON_SOFTMAX
+    a.dtype = _lib.DTYPE_CODES[q.dtype]
+    a.B, a.H, a.T, a.D, a.L = B, H, T, dp, L
+    a.gamma = float(sm_scale)
+    a.q, a.k, a.v, a.o = (_lib.tensor_desc(t) for t in (q_, k_, v_, out))
+    lens = None
+    if cache_lens is not None:
+        lens = cache_lens.to(device=q.device, dtype=torch.int32).contiguous()
+        if lens.shape != (B,):
+            raise ValueError(f"decode: cache_lens must have shape ({B},)")
+        a.lens = lens.data_ptr()
+    a.lse = lse.data_ptr() if softmax else None
+    nbytes = _lib.decode_workspace_size(a)
+    ws = torch.empty((nbytes + 15) // 16 * 4, device=q.device, dtype=torch.float32)
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = nbytes
+    with torch.cuda.device(q.device):
+        _lib.call("rbf_attn_decode", a, torch.cuda.current_stream(q.device).cuda_stream)
+    return _unpad(out, D), lse
+
+
+@torch.library.custom_op(f"{_EX}::decode", mutates_args=())
+def rbf_decode_op(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    cache_lens: torch.Tensor | None,
+    softmax: bool,
+    sm_scale: float,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    return _decode(q, k_cache, v_cache, cache_lens, softmax, sm_scale)
+
+
+@rbf_decode_op.register_fake
+def _(q, k_cache, v_cache, cache_lens, softmax, sm_scale):
+    B, H, T, _ = q.shape
+    return torch.empty_like(q, memory_format=torch.contiguous_format), torch.empty(
+        (B, H, T), device=q.device, dtype=torch.float32
+    )
+
+
+def rbf_decode(q, k_cache, v_cache, cache_lens=None, *, softmax=True, sm_scale=None):
+    """Attention of T new query tokens (q: (B, H, T, D), 1 <= T <= 32) against
+    a KV cache (B, H, L, D) that already holds their keys and values.  Query t
+    of batch b sits at position cache_lens[b] - T + t (cache_lens defaults to
+    L for every b) and sees keys [0, that position].  Returns (out, L) with L
+    the base-2 log-sum-exp (softmax; unspecified for the non-softmax variant).
+    Forward only."""
+    scale = _default_scale(q) if sm_scale is None else float(sm_scale)
+    return torch.ops.rbf_attn_amd.decode(q, k_cache, v_cache, cache_lens, bool(softmax), scale)
+
+
+# ---------------------------------------------------------------------------
 # Public wrappers (rbf_attention.py:848-853) and autograd.Function aliases.
 # ---------------------------------------------------------------------------
-def run_triton_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0):
-    """Softmax RBF attention.  With the default ``sm_scale`` (1/sqrt(D)) and
-    ``num_prefix=0`` this is exactly the reference's ``run_triton_rbf``."""
-    if sm_scale is None and num_prefix == 0:
+def run_triton_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, token_major=False):
+    """Softmax RBF attention.  With the default ``sm_scale`` (1/sqrt(D)),
+    ``num_prefix=0`` and ``token_major=False`` this is exactly the reference's
+    ``run_triton_rbf``.  ``token_major=True`` returns the (B, H, N, D) output as
+    a view of a (B, N, H, D) buffer (see ``_alloc_out``)."""
+    if sm_scale is None and num_prefix == 0 and not token_major:
         return torch.ops.rbf_attn_v5.scaled_fwd(q, k, v, is_causal)[0]
     scale = _default_scale(q) if sm_scale is None else float(sm_scale)
-    return torch.ops.rbf_attn_amd.scaled_fwd_ex(q, k, v, is_causal, scale, int(num_prefix))[0]
+    return torch.ops.rbf_attn_amd.scaled_fwd_ex(q, k, v, is_causal, scale, int(num_prefix), bool(token_major))[0]
 
 
-def run_triton_non_softmax_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0):
+def run_triton_non_softmax_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, token_major=False):
     """Non-softmax RBF attention, sum_j exp(-gamma||q_i-k_j||^2) v_j."""
-    if sm_scale is None and num_prefix == 0:
+    if sm_scale is None and num_prefix == 0 and not token_major:
         return torch.ops.rbf_attn_v5.non_softmax_fwd(q, k, v, is_causal)
     scale = _default_scale(q) if sm_scale is None else float(sm_scale)
-    return torch.ops.rbf_attn_amd.non_softmax_fwd_ex(q, k, v, is_causal, scale, int(num_prefix))
+    return torch.ops.rbf_attn_amd.non_softmax_fwd_ex(q, k, v, is_causal, scale, int(num_prefix), bool(token_major))
 
 
 class TritonRBFAttention(torch.autograd.Function):

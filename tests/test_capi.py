@@ -128,3 +128,56 @@ def test_empty_problem_is_noop(lib):
         assert call(lib, "rbf_attn_fwd", good_args(**over)) == 0
         assert call(lib, "rbf_attn_bwd", good_args(**over)) == 0
         assert lib.rbf_attn_last_error().decode() == ""
+
+
+# ---------------------------------------------------------------------------
+# decode entry points
+# ---------------------------------------------------------------------------
+def test_decode_struct_layout():
+    # 9 int32/float fields, padding, 4 tensors, 3 pointers, one uint64
+    assert _lib.DecodeArgs.q.offset == 40
+    assert _lib.DecodeArgs.lens.offset == 40 + 4 * 32
+    assert ctypes.sizeof(_lib.DecodeArgs) == 40 + 4 * 32 + 4 * 8
+
+
+def decode_args(**over):
+    a = _lib.DecodeArgs()
+    a.abi_version, a.variant, a.dtype = _lib.ABI_VERSION, 0, 0
+    a.B, a.H, a.T, a.D, a.L = 2, 3, 1, 64, 1000
+    a.gamma = 0.0625
+    for f in ("q", "k", "v", "o"):
+        setattr(a, f, _lib.Tensor(FAKE, 64 * 4096, 64 * 1024, 64))
+    for kk, vv in over.items():
+        setattr(a, kk, vv)
+    return a
+
+
+def test_decode_workspace_size(lib):
+    # 6 (b, h) pairs want ~1024 work-groups but 1000 keys make only 8 tiles
+    # of 128: 8 splits x 4 waves = 32 partials of (64 + 2) floats per query.
+    assert lib.rbf_attn_decode_workspace_size(ctypes.byref(decode_args())) == 6 * 32 * 1 * 66 * 4
+    # fp32 runs 2 waves per 64-key tile: 16 tiles, 16 splits
+    assert lib.rbf_attn_decode_workspace_size(ctypes.byref(decode_args(dtype=2))) == 6 * 32 * 1 * 66 * 4
+
+
+@pytest.mark.parametrize("over", [dict(T=0), dict(T=33), dict(L=0), dict(T=4, L=3), dict(D=12), dict(D=136),
+                                  dict(gamma=0.0), dict(variant=2), dict(dtype=5), dict(abi_version=0)])
+def test_decode_validation(lib, over):
+    a = decode_args(**over)
+    assert lib.rbf_attn_decode_workspace_size(ctypes.byref(a)) == 0
+    assert lib.rbf_attn_last_error() != b""
+    assert lib.rbf_attn_decode(ctypes.byref(a), None) < 0
+
+
+def test_decode_workspace_checks(lib):
+    a = decode_args()
+    assert lib.rbf_attn_decode(ctypes.byref(a), None) == header_define("RBF_ATTN_EINVAL_PTR")
+    a.workspace, a.workspace_bytes = FAKE, 100
+    assert lib.rbf_attn_decode(ctypes.byref(a), None) == header_define("RBF_ATTN_EINVAL_ARGS")
+    b = decode_args(q=_lib.Tensor(FAKE + 8, 0, 0, 64))
+    assert lib.rbf_attn_decode(ctypes.byref(b), None) == header_define("RBF_ATTN_EINVAL_STRIDE")
+
+
+def test_decode_empty_batch_is_noop(lib):
+    a = decode_args(B=0)
+    assert lib.rbf_attn_decode(ctypes.byref(a), None) == 0

@@ -148,6 +148,28 @@ def pin_finite_differences(o, softmax=True):
     return True
 
 
+def pin_decode_vs_forward(o, softmax=True, ragged=False):
+    """Decode = the last T query rows of the causal forward over the first
+    lens[b] cached tokens (the forward itself is pinned above)."""
+    B, H, L, T, D = 2, 2, 23, 3, 8
+    qf, k, v = rand(B, H, L, D), rand(B, H, L, D, scale=1.3), rand(B, H, L, D)
+    g = 0.17
+    lens = [L, 14] if ragged else [L, L]
+    qd = np.stack([qf[b, :, lens[b] - T:lens[b]] for b in range(B)])
+    O, Ld = o.decode_forward(qd, k, v, g, softmax, lens if ragged else None)
+    for b in range(B):
+        n = lens[b]
+        if softmax:
+            Of, Lf = o.softmax_forward(qf[b:b + 1, :, :n], k[b:b + 1, :, :n], v[b:b + 1, :, :n], g)
+            if np.abs(Ld[b] - Lf[0, :, n - T:]).max() > 1e-12:
+                return False
+        else:
+            Of = o.non_softmax_forward(qf[b:b + 1, :, :n], k[b:b + 1, :, :n], v[b:b + 1, :, :n], g)
+        if np.abs(O[b] - Of[0, :, n - T:]).max() > 1e-12:
+            return False
+    return True
+
+
 ALL_PINS = [
     lambda o: pin_forward_vs_augmented(o),
     lambda o: pin_forward_vs_augmented(o, num_prefix=4),
@@ -169,6 +191,9 @@ ALL_PINS = [
     lambda o: pin_lse(o, num_prefix=2),
     lambda o: pin_finite_differences(o, softmax=True),
     lambda o: pin_finite_differences(o, softmax=False),
+    lambda o: pin_decode_vs_forward(o, softmax=True),
+    lambda o: pin_decode_vs_forward(o, softmax=True, ragged=True),
+    lambda o: pin_decode_vs_forward(o, softmax=False, ragged=True),
 ]
 
 
@@ -261,6 +286,8 @@ MUTATIONS = {
     "lse_missing_qnorm": ("L[b, h] = (m + np.log(l) + gamma * np.einsum(\"nd,nd->n\", qs, qs)) * LOG2E",
                           "L[b, h] = (m + np.log(l)) * LOG2E"),
     "augment_wrong_half": ("kp = np.concatenate([k, -0.5 * kk], axis=-1)", "kp = np.concatenate([k, -kk], axis=-1)"),
+    "decode_position_off_by_one": ("pos = np.arange(n - T, n)[:, None]", "pos = np.arange(n - T - 1, n - 1)[:, None]"),
+    "decode_ignores_lengths": ("lens = [Lc] * B if lens is None else [int(x) for x in lens]", "lens = [Lc] * B"),
 }
 
 

@@ -225,6 +225,26 @@ def test_queries_far_from_every_key(cuda_device, dtype, shift):
     compare_case(q, k, v, do, gamma=0.0625, tag=f"far{shift} {dtype}")
 
 
+@pytest.mark.parametrize("softmax", [True, False])
+def test_token_major_output(cuda_device, softmax):
+    """token_major=True: same values and gradients bit for bit, and the model's
+    (B, H, N, D) -> (B, N, H*D) transpose + reshape is a view."""
+    q, k, v, do = rand_inputs(2, 4, 100, 64, torch.bfloat16, cuda_device, std=1.0 if softmax else 0.5, seed=5)
+    fn = ra.run_triton_rbf if softmax else ra.run_triton_non_softmax_rbf
+    res = []
+    for tm in (False, True):
+        qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        out = fn(qq, kk, vv, True, sm_scale=0.0625, token_major=tm)
+        flat = out.transpose(1, 2).reshape(2, 100, 4 * 64)
+        if tm:
+            assert flat.data_ptr() == out.data_ptr() and flat.is_contiguous()
+        flat.backward(do.transpose(1, 2).reshape(2, 100, 256))
+        torch.cuda.synchronize()
+        res.append((out.detach(), qq.grad, kk.grad, vv.grad))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
+
 def test_strided_views_like_the_model(cuda_device):
     """q/k/v as views of one packed projection, dout as a permuted view
     (rbf_attention.py:1659-1662, 1761)."""
