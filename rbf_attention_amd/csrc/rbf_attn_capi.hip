@@ -5,6 +5,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <hip/hip_runtime.h>
 
@@ -108,6 +109,18 @@ rbf::Params make_params(const rbf_attn_args* a) {
   const int rem = a->N % 32;
   p.org = rem == 0 ? 0 : rem - 32;
   p.nblk = (a->N - p.org) / 32;
+  // Heaviest-group-first chunks of heads on one XCD: as many heads as have
+  // 8 MB of streamed operands (K and V, or Q and dO) between them.  Measured
+  // on MI355X: short heads want the whole XCD share in one chunk (no heavy
+  // group left for the end of the launch), 4 MB heads want head-major order
+  // (their groups share K/V in L2 while they run together).
+  const long long per_head = 2LL * a->N * a->D * (long long)elem_size(a->dtype);
+  const long long fit = per_head > 0 ? (8LL << 20) / per_head : 1;
+  const long long per_xcd = ((long long)a->B * a->H) / 8;
+  p.hchunk = (int)(fit < 1 ? 1 : (fit > per_xcd ? (per_xcd > 0 ? per_xcd : 1) : fit));
+  // RBF_ATTN_HCHUNK overrides the chunk size (tuning sweeps).
+  static const int forced = getenv("RBF_ATTN_HCHUNK") ? atoi(getenv("RBF_ATTN_HCHUNK")) : 0;
+  if (forced > 0) p.hchunk = (int)(forced < per_xcd ? forced : (per_xcd > 0 ? per_xcd : 1));
   return p;
 }
 

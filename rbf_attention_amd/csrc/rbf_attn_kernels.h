@@ -71,6 +71,7 @@ struct Params {
   float c;           // 2 * gamma * log2(e)
   int org;           // first token of block 0 (<= 0)
   int nblk;          // number of 32-token blocks
+  int hchunk;        // heads per heaviest-first chunk on one XCD (>= 1)
 };
 
 // ---------------------------------------------------------------------------
@@ -514,18 +515,36 @@ struct TileLayout {
   }
 };
 
-// Work-group -> (b*H + h, group) with an XCD-aware remap: the hardware deals
-// work-groups round-robin over the 8 XCDs, so consecutive logical indices
-// (the groups of one head, which share K/V or Q/dO) are packed onto the same
-// XCD to share its L2.
-__device__ inline void decode_wg(int ngrp, bool reverse, int& bh, int& grp) {
+// Work-group -> (b*H + h, group).  The hardware deals work-groups
+// round-robin over the 8 XCDs (block id mod 8) and each XCD starts its share
+// in block-id order.  When B*H is a multiple of 8, XCD x owns whole heads
+// [x*BH/8, (x+1)*BH/8), so the groups of a head share K/V (or Q/dO) in that
+// XCD's L2.  The XCD's heads are taken in chunks of `hchunk` heads -- as many
+// as the host expects to fit in L2 together -- and inside a chunk the
+// heaviest group of every head runs first, then every head's second
+// heaviest, and so on, so that no heavy group is left for the end of the
+// launch.  Group weight falls with the group index when `reverse` is false
+// (dK/dV: early keys see the most queries) and rises with it when true
+// (causal forward and dQ).
+__device__ inline void decode_wg(int ngrp, bool reverse, int hchunk, int& bh, int& grp) {
   const int total = gridDim.x;
   const int bid = blockIdx.x;
-  int L = bid;
-  if ((total & 7) == 0) L = (bid & 7) * (total >> 3) + (bid >> 3);
-  bh = L / ngrp;
-  const int j = L - bh * ngrp;
-  grp = reverse ? (ngrp - 1 - j) : j;
+  const int BH = total / ngrp;
+  int rank;
+  if ((BH & 7) == 0) {
+    const int per_xcd = BH >> 3;
+    const int local = bid >> 3;
+    const int chunk = local / (hchunk * ngrp);
+    const int h0 = chunk * hchunk;
+    const int nh = min(hchunk, per_xcd - h0);
+    const int r = local - h0 * ngrp;
+    rank = r / nh;
+    bh = (bid & 7) * per_xcd + h0 + (r - rank * nh);
+  } else {
+    bh = bid / ngrp;
+    rank = bid - bh * ngrp;
+  }
+  grp = reverse ? (ngrp - 1 - rank) : rank;
 }
 
 // Visibility of a 32x32 (query block, key block) pair: `any` if at least one
@@ -653,7 +672,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   const float c = p.c;
   const int ngrp = (nblk + W - 1) / W;
   int bh, grp;
-  decode_wg(ngrp, causal, bh, grp);
+  decode_wg(ngrp, causal, p.hchunk, bh, grp);
   const int b = bh / p.H, hh = bh - b * p.H;
   const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
   const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
@@ -834,7 +853,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   const float c = p.c;
   const int ngrp = (nblk + GB - 1) / GB;
   int bh, grp;
-  decode_wg(ngrp, causal, bh, grp);
+  decode_wg(ngrp, causal, p.hchunk, bh, grp);
   const int b = bh / p.H, hh = bh - b * p.H;
   const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
   const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
@@ -1067,7 +1086,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   const float inv_c = 1.f / c;
   const int ngrp = (nblk + GB - 1) / GB;
   int bh, grp;
-  decode_wg(ngrp, false, bh, grp);
+  decode_wg(ngrp, false, p.hchunk, bh, grp);
   const int b = bh / p.H, hh = bh - b * p.H;
   const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
   const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
@@ -1373,7 +1392,7 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
   const float inv_c = 1.f / c;
   const int ngrp = (nblk + NP - 1) / NP;
   int bh, grp;
-  decode_wg(ngrp, false, bh, grp);
+  decode_wg(ngrp, false, p.hchunk, bh, grp);
   const int b = bh / p.H, hh = bh - b * p.H;
   const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
   const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
