@@ -6,10 +6,11 @@
 // keys [0, len_b - T + t] (the cache already holds the new tokens' K and V).
 //
 //   rbf_decode_split_kernel: grid (B*H, nsplit), W waves per work-group.  A
-//     work-group streams its split's 32*W-key tiles of K, V (and -0.5||k||^2)
-//     through double-buffered LDS; wave w owns the w-th 32-key block of every
-//     tile and keeps its own partial (m, l, O^T) for the T queries, with the
-//     online max of the forward kernel.  Each wave writes its partial to the
+//     work-group streams its split's 32*W-key tiles of V through
+//     double-buffered LDS; wave w owns the w-th 32-key block of every tile,
+//     loads that block's K rows straight into registers (one tile ahead) and
+//     keeps its own partial (m, l, O^T) for the T queries, with the online
+//     max of the forward kernel.  Each wave writes its partial to the
 //     workspace.
 //   rbf_decode_merge_kernel: one wave per (b, h, t) combines the partials:
 //     O = sum_p 2^(m_p - M) o_p / sum_p 2^(m_p - M) l_p, L = M + log2(l).
@@ -46,12 +47,14 @@ __global__ __launch_bounds__(64 * W) void rbf_decode_split_kernel(const DecodePa
   typedef Elem<T> E;
   typedef typename E::frag frag;
   constexpr int BN = 32 * W, NT = 64 * W, KS = DP / 16, ND = DP / 32;
-  constexpr int LDR = DP + E::PAD, LDT = BN + E::PAD;
+  constexpr int LDT = BN + E::PAD;
   constexpr bool TR = sizeof(T) == 2;
   typedef TileLayout<T, BN, DP> TLy;
-  __shared__ __attribute__((aligned(16))) T sK[2][TLy::SIZE];
+  // Only V goes through LDS (it is read transposed); each wave loads the K
+  // rows of its own 32-key block straight into MFMA operand registers, one
+  // tile ahead, and derives the key norms from them.
   __shared__ __attribute__((aligned(16))) T sVt[2][TR ? TLy::SIZE : DP * LDT];
-  __shared__ __attribute__((aligned(16))) float sKn[2][BN];
+  __shared__ __attribute__((aligned(16))) float sKn[W][32];
 
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -76,41 +79,44 @@ __global__ __launch_bounds__(64 * W) void rbf_decode_split_kernel(const DecodePa
     qn2 += sumsq8<T>(qf[t]);
   }
   qn2 = c * 0.5f * xhalf_sum(qn2);
-  const frag onesA = ones_row_frag<T>(n);
-
-  f32x16_t oacc[ND], lacc = zero16();
+  f32x16_t oacc[ND];
+  float lsum = 0.f;  // this lane's share of the row sum (VALU; decode is HBM-bound)
 #pragma unroll
   for (int d = 0; d < ND; ++d) oacc[d] = zero16();
   float m_run = SOFTMAX ? -__builtin_inff() : qn2;
 
-  TileFor<T, BN, DP, NT> tk, tv;
+  frag kA[KS];
+  auto load_k = [&](int kt) {
+    const int tok = kt * BN + 32 * wave + n;
+    const bool ok = tok < len;
+#pragma unroll
+    for (int t = 0; t < KS; ++t)
+      kA[t] = (ok && 16 * t + 8 * h < D) ? ld8<T>(K + (int64_t)tok * p.sk[2] + 16 * t + 8 * h) : zero_frag<T>();
+  };
+  TileFor<T, BN, DP, NT> tv;
   if (kt0 < kt1) {
-    tk.load(K, p.sk[2], kt0 * BN, len, D, tid);
+    load_k(kt0);
     tv.load(V, p.sv[2], kt0 * BN, len, D, tid);
   }
   for (int kt = kt0; kt < kt1; ++kt) {
     const int buf = kt & 1;
-    if constexpr (TR) {
-      TLy::store(tk, sK[buf], tid);
-      TLy::store(tv, sVt[buf], tid);
-    } else {
-      tk.template store_rows<LDR>(sK[buf], tid);
-      tv.template store_trans<LDT>(sVt[buf], tid);
-    }
-    tk.store_neg_halfnorm(sKn[buf], tid);
+    if constexpr (TR) TLy::store(tv, sVt[buf], tid);
+    else tv.template store_trans<LDT>(sVt[buf], tid);
     __syncthreads();
-    if (kt + 1 < kt1) {
-      tk.load(K, p.sk[2], (kt + 1) * BN, len, D, tid);
-      tv.load(V, p.sv[2], (kt + 1) * BN, len, D, tid);
-    }
+    if (kt + 1 < kt1) tv.load(V, p.sv[2], (kt + 1) * BN, len, D, tid);
     const int k0 = kt * BN + 32 * wave;
     if (k0 >= len) continue;  // wave-uniform: the block lies past the cache
-    frag kA[KS];
+    // -0.5||k||^2 of this lane's key, transposed to the accumulator's rows
+    // through the wave's own LDS slot (-inf past the cache length)
+    float kn = 0.f;
 #pragma unroll
-    for (int t = 0; t < KS; ++t) kA[t] = ld8<T>(sK[buf] + TLy::off(32 * wave + n, 16 * t + 8 * h));
-    f32x16_t s = ld_rows16(sKn[buf] + 32 * wave, h);  // -inf for keys >= len
+    for (int t = 0; t < KS; ++t) kn += sumsq8<T>(kA[t]);
+    kn = xhalf_sum(kn);
+    if (h == 0) sKn[wave][n] = (k0 + n < len) ? -0.5f * kn : -__builtin_inff();
+    f32x16_t s = ld_rows16(sKn[wave], h);
 #pragma unroll
     for (int t = 0; t < KS; ++t) s = E::mma(kA[t], qf[t], s);
+    if (kt + 1 < kt1) load_k(kt + 1);  // kA is free once the S products are issued
     frag vA[ND][2];
 #pragma unroll
     for (int d = 0; d < ND; ++d)
@@ -127,20 +133,23 @@ __global__ __launch_bounds__(64 * W) void rbf_decode_split_kernel(const DecodePa
         const float alpha = (mnew == -__builtin_inff()) ? 1.f : fast_exp2(m_run - mnew);
 #pragma unroll
         for (int d = 0; d < ND; ++d) oacc[d] *= alpha;
-        lacc *= alpha;
+        lsum *= alpha;
         m_run = mnew;
       }
     }
     const float moff = (SOFTMAX && m_run == -__builtin_inff()) ? 0.f : m_run;
     frag pf[2];
+    float pv[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) pf[i >> 3][i & 7] = (T)fast_exp2(fmaf(s[i], c, -moff));
+    for (int i = 0; i < 16; ++i) {
+      pf[i >> 3][i & 7] = (T)fast_exp2(fmaf(s[i], c, -moff));
+      pv[i] = (float)pf[i >> 3][i & 7];  // the rounded P the numerator uses
+    }
+    if constexpr (SOFTMAX) lsum += tree_sum16(pv);
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int d = 0; d < ND; ++d) oacc[d] = E::mma(vA[d][t], pf[t], oacc[d]);
-      if constexpr (SOFTMAX) lacc = E::mma(onesA, pf[t], lacc);
-    }
   }
 
   // partial of this wave
@@ -156,7 +165,7 @@ __global__ __launch_bounds__(64 * W) void rbf_decode_split_kernel(const DecodePa
       f32x4_t v4 = {oacc[d][4 * g], oacc[d][4 * g + 1], oacc[d][4 * g + 2], oacc[d][4 * g + 3]};
       *reinterpret_cast<f32x4_t*>(wo + dd) = v4;
     }
-  const float l = SOFTMAX ? xhalf_sum(lacc[0]) : 0.f;
+  const float l = SOFTMAX ? xhalf_sum(lsum) : 0.f;
   if (h == 0) {
     float* wm = p.ws + (int64_t)p.B * p.H * P * Tq * DP;
     float* wl = wm + (int64_t)p.B * p.H * P * Tq;

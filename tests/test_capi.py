@@ -153,11 +153,14 @@ def decode_args(**over):
 
 
 def test_decode_workspace_size(lib):
-    # 6 (b, h) pairs want ~1024 work-groups but 1000 keys make only 8 tiles
-    # of 128: 8 splits x 4 waves = 32 partials of (64 + 2) floats per query.
+    # 6 (b, h) pairs want hundreds of work-groups but 1000 keys make only 8
+    # tiles of 128: 8 splits x 4 waves = 32 partials of (64 + 2) floats per query.
     assert lib.rbf_attn_decode_workspace_size(ctypes.byref(decode_args())) == 6 * 32 * 1 * 66 * 4
     # fp32 runs 2 waves per 64-key tile: 16 tiles, 16 splits
     assert lib.rbf_attn_decode_workspace_size(ctypes.byref(decode_args(dtype=2))) == 6 * 32 * 1 * 66 * 4
+    # 128 (b, h) pairs, 16K keys, 128 features: 512 work-groups = 4 splits
+    big = decode_args(B=8, H=16, T=1, D=128, L=16384)
+    assert lib.rbf_attn_decode_workspace_size(ctypes.byref(big)) == 128 * 16 * 1 * 130 * 4
 
 
 @pytest.mark.parametrize("over", [dict(T=0), dict(T=33), dict(L=0), dict(T=4, L=3), dict(D=12), dict(D=136),
