@@ -86,7 +86,7 @@ template <int DP, bool SM>
 hipError_t dq_default(const Params& p, hipStream_t st) {
   if constexpr (kIsF32) return dq_cfg<DP, SM, 4, 1, 32>(p, st);
   else if constexpr (DP <= 64) return dq_cfg<DP, SM, 4, 1, 128>(p, st);
-  else return dq_cfg<DP, SM, 4, 1, 32>(p, st);
+  else return dq_cfg<DP, SM, 8, 1, 32>(p, st);
 }
 
 template <int DP, bool SM>
@@ -124,6 +124,8 @@ hipError_t dq_any_cfg(const Params& p, hipStream_t st) {
     switch (choice) {
       case 8: return dq_cfg<DP, SM, 4, 1, 64>(p, st);
       case 9: return dq_cfg<DP, SM, 4, 1, 32, false>(p, st);
+      case 10: return dq_cfg<DP, SM, 8, 1, 32>(p, st);
+      case 11: return dq_cfg<DP, SM, 8, 1, 32, false>(p, st);
       default: break;
     }
   }
