@@ -72,6 +72,7 @@ struct Params {
   int org;           // first token of block 0 (<= 0)
   int nblk;          // number of 32-token blocks
   int hchunk;        // heads per heaviest-first chunk on one XCD (>= 1)
+  int nbin;          // work-groups per head (set per launch; each runs a bin of groups)
 };
 
 // ---------------------------------------------------------------------------
@@ -515,36 +516,53 @@ struct TileLayout {
   }
 };
 
-// Work-group -> (b*H + h, group).  The hardware deals work-groups
-// round-robin over the 8 XCDs (block id mod 8) and each XCD starts its share
-// in block-id order.  When B*H is a multiple of 8, XCD x owns whole heads
-// [x*BH/8, (x+1)*BH/8), so the groups of a head share K/V (or Q/dO) in that
-// XCD's L2.  The XCD's heads are taken in chunks of `hchunk` heads -- as many
-// as the host expects to fit in L2 together -- and inside a chunk the
-// heaviest group of every head runs first, then every head's second
-// heaviest, and so on, so that no heavy group is left for the end of the
-// launch.  Group weight falls with the group index when `reverse` is false
-// (dK/dV: early keys see the most queries) and rises with it when true
-// (causal forward and dQ).
-__device__ inline void decode_wg(int ngrp, bool reverse, int hchunk, int& bh, int& grp) {
+// Work-group -> (b*H + h, bin).  The hardware deals work-groups round-robin
+// over the 8 XCDs (block id mod 8) and each XCD starts its share in block-id
+// order.  When B*H is a multiple of 8, XCD x owns whole heads
+// [x*BH/8, (x+1)*BH/8), so the work-groups of a head share K/V (or Q/dO) in
+// that XCD's L2.  The XCD's heads are taken in chunks of `hchunk` heads -- as
+// many as the host expects to fit in L2 together -- and inside a chunk bin 0
+// of every head runs first, then every head's bin 1, and so on.
+__device__ inline void decode_wg(int nbin, int hchunk, int& bh, int& bin) {
   const int total = gridDim.x;
   const int bid = blockIdx.x;
-  const int BH = total / ngrp;
-  int rank;
+  const int BH = total / nbin;
   if ((BH & 7) == 0) {
     const int per_xcd = BH >> 3;
     const int local = bid >> 3;
-    const int chunk = local / (hchunk * ngrp);
+    const int chunk = local / (hchunk * nbin);
     const int h0 = chunk * hchunk;
     const int nh = min(hchunk, per_xcd - h0);
-    const int r = local - h0 * ngrp;
-    rank = r / nh;
-    bh = (bid & 7) * per_xcd + h0 + (r - rank * nh);
+    const int r = local - h0 * nbin;
+    bin = r / nh;
+    bh = (bid & 7) * per_xcd + h0 + (r - bin * nh);
   } else {
-    bh = bid / ngrp;
-    rank = bid - bh * ngrp;
+    bh = bid / nbin;
+    bin = bid - bh * nbin;
   }
-  grp = reverse ? (ngrp - 1 - rank) : rank;
+}
+
+// Runs f(bh, group) for every group of this work-group's bin.  A head's
+// `ngrp` groups are ranked by causal weight, heaviest first (the weight
+// rises with the group index when `reverse` is true -- causal forward and dQ
+// -- and falls with it otherwise -- dK/dV, whose early keys see the most
+// queries), and dealt to the head's `p.nbin` bins in boustrophedon order:
+// ranks 0..R-1 to bins 0..R-1, ranks R..2R-1 to bins R-1..0, and so on.  With
+// R = ngrp every bin holds one group (heaviest bins first in launch order);
+// with fewer bins the host picks R so that all work-groups run at once and
+// the snake order gives them near-equal causal work.  The bin's groups run
+// back to back, separated by a barrier (they reuse the LDS tiles).
+template <typename F>
+__device__ __forceinline__ void for_each_group(const Params& p, int ngrp, bool reverse, F&& f) {
+  const int nbin = (p.nbin > 0 && p.nbin < ngrp) ? p.nbin : ngrp;
+  int bh, bin;
+  decode_wg(nbin, p.hchunk, bh, bin);
+  for (int k = 0;; ++k) {
+    const int rank = k * nbin + ((k & 1) ? nbin - 1 - bin : bin);
+    if (rank >= ngrp) break;
+    if (k) __syncthreads();
+    f(bh, reverse ? ngrp - 1 - rank : rank);
+  }
 }
 
 // Visibility of a 32x32 (query block, key block) pair: `any` if at least one
@@ -648,7 +666,7 @@ constexpr float kBoundMargin = 60.f;  // P <= 2^60 under the static bound
 constexpr float kSumLow = 0x1p-60f, kSumHigh = 0x1p100f;
 
 template <typename T, int DP, int W, int BN, bool SOFTMAX>
-__global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
+__device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   constexpr int NT = 64 * W, KB = BN / 32, KS = DP / 16, ND = DP / 32;
@@ -671,8 +689,6 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   const int npre = p.num_prefix;
   const float c = p.c;
   const int ngrp = (nblk + W - 1) / W;
-  int bh, grp;
-  decode_wg(ngrp, causal, p.hchunk, bh, grp);
   const int b = bh / p.H, hh = bh - b * p.H;
   const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
   const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
@@ -819,6 +835,15 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
   if (SOFTMAX && h == 0) p.lse[(int64_t)bh * N + qtok] = m_run + __log2f(lsum);
 }
 
+// WPE > 0 asks the compiler for at least WPE waves per SIMD (register
+// budget 512 / WPE): the 16-bit D <= 64 forward keeps three, as it has without
+// the bin loop around its body.
+template <typename T, int DP, int W, int BN, bool SOFTMAX, int WPE = (sizeof(T) == 2 && DP <= 64) ? 3 : 1>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void rbf_fwd_kernel(const Params p) {
+  for_each_group(p, (p.nblk + W - 1) / W, p.causal != 0,
+                 [&](int bh, int grp) { rbf_fwd_group<T, DP, W, BN, SOFTMAX>(p, bh, grp); });
+}
+
 // ---------------------------------------------------------------------------
 // Backward, query-stationary: dQ.  A wave owns QPW query blocks.  Also
 // produces, per query, Delta = rowsum(O*dO) (softmax) or the norm offset
@@ -829,7 +854,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_kernel(const Params p) {
 //   dP^T = V dO^T (init -Delta), dS = P dP^T, dQ^T += K^T dS^T.
 // ---------------------------------------------------------------------------
 template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX, bool EARLY = true>
-__global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
+__device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int grp) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   constexpr int NT = 64 * W, KB = BN / 32, KS = DP / 16, ND = DP / 32, GB = W * QPW;
@@ -852,8 +877,6 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   const int npre = p.num_prefix;
   const float c = p.c;
   const int ngrp = (nblk + GB - 1) / GB;
-  int bh, grp;
-  decode_wg(ngrp, causal, p.hchunk, bh, grp);
   const int b = bh / p.H, hh = bh - b * p.H;
   const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
   const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
@@ -1047,6 +1070,12 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   }
 }
 
+template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX, bool EARLY = true>
+__global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
+  for_each_group(p, (p.nblk + W * QPW - 1) / (W * QPW), p.causal != 0,
+                 [&](int bh, int grp) { rbf_bwd_dq_group<T, DP, W, QPW, BN, SOFTMAX, EARLY>(p, bh, grp); });
+}
+
 // ---------------------------------------------------------------------------
 // Backward, key-stationary: dK and dV.  A wave owns KPW key blocks (K and V
 // fragments in registers); BM-query tiles of Q and dO (row-major and
@@ -1059,7 +1088,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
 // ---------------------------------------------------------------------------
 template <typename T, int DP, int W, int KPW, int BM, bool SOFTMAX, bool EARLY = true, bool PIPE = false,
           bool PRIO = false>
-__global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
+__device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int grp) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   constexpr int NT = 64 * W, QB = BM / 32, KS = DP / 16, ND = DP / 32, GB = W * KPW;
@@ -1085,8 +1114,6 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   const float c = p.c;
   const float inv_c = 1.f / c;
   const int ngrp = (nblk + GB - 1) / GB;
-  int bh, grp;
-  decode_wg(ngrp, false, p.hchunk, bh, grp);
   const int b = bh / p.H, hh = bh - b * p.H;
   const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
   const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
@@ -1350,6 +1377,13 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   }
 }
 
+template <typename T, int DP, int W, int KPW, int BM, bool SOFTMAX, bool EARLY = true, bool PIPE = false,
+          bool PRIO = false>
+__global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
+  for_each_group(p, (p.nblk + W * KPW - 1) / (W * KPW), false,
+                 [&](int bh, int grp) { rbf_bwd_dkdv_group<T, DP, W, KPW, BM, SOFTMAX, EARLY, PIPE, PRIO>(p, bh, grp); });
+}
+
 // ---------------------------------------------------------------------------
 // Backward, key-stationary, two waves per key block (16-bit types).  A
 // work-group holds NP key blocks and 2*NP waves: wave j (< NP) is the P-wave
@@ -1369,7 +1403,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
 // LDS latency.
 // ---------------------------------------------------------------------------
 template <typename T, int DP, int NP, int BM, bool SOFTMAX, bool SGB = false>
-__global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Params p) {
+__device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh, int grp) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   static_assert(sizeof(T) == 2, "the paired kernel reads transposed operands with ds_read_b64_tr_b16");
@@ -1391,8 +1425,6 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
   const float c = p.c;
   const float inv_c = 1.f / c;
   const int ngrp = (nblk + NP - 1) / NP;
-  int bh, grp;
-  decode_wg(ngrp, false, p.hchunk, bh, grp);
   const int b = bh / p.H, hh = bh - b * p.H;
   const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
   const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
@@ -1575,6 +1607,12 @@ __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Param
         st4f<T>(orow + dd, a4);
       }
     }
+}
+
+template <typename T, int DP, int NP, int BM, bool SOFTMAX, bool SGB = false>
+__global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Params p) {
+  for_each_group(p, (p.nblk + NP - 1) / NP, false,
+                 [&](int bh, int grp) { rbf_bwd_dkdv_pair_group<T, DP, NP, BM, SOFTMAX, SGB>(p, bh, grp); });
 }
 
 }  // namespace rbf

@@ -30,41 +30,84 @@ typedef float Elt;
 
 constexpr bool kIsF32 = sizeof(Elt) == 4;
 
-inline unsigned grid_of(const Params& p, int blocks_per_wg) {
+int env_choice(const char* name) {
+  const char* s = getenv(name);
+  return s ? atoi(s) : -1;
+}
+
+int cu_count() {
+  static const int n = [] {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      v = 256;
+    return v > 0 ? v : 256;
+  }();
+  return n;
+}
+
+template <typename F>
+int wgs_per_cu(F kernel, int threads) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n < 1) n = 1;
+  return n;
+}
+
+// Work-groups per head (Params::nbin) and the grid.  A head has `ngrp`
+// groups of `blocks_per_wg` 32-token blocks.  When every group fits on the
+// GPU at once each gets its own work-group; otherwise the groups are dealt
+// to as many bins per head as keep all work-groups resident together
+// (`wgs` per CU), so that the launch runs in one round of near-equal
+// work-groups instead of a heavy round followed by a tail of light, short
+// ones.  RBF_ATTN_NBIN=n forces n bins per head (0: one group per bin).
+unsigned set_bins(Params& p, int blocks_per_wg, int wgs) {
   const int ngrp = (p.nblk + blocks_per_wg - 1) / blocks_per_wg;
-  return (unsigned)((long long)p.B * p.H * ngrp);
+  const long long BH = (long long)p.B * p.H;
+  static const int forced = env_choice("RBF_ATTN_NBIN");
+  long long nbin = ngrp;
+  if (forced > 0) {
+    nbin = forced < ngrp ? forced : ngrp;
+  } else if (forced < 0 && BH > 0) {
+    const long long slots = (long long)cu_count() * wgs;
+    if (BH * ngrp > slots) nbin = slots / BH < 1 ? 1 : (slots / BH < ngrp ? slots / BH : ngrp);
+  }
+  p.nbin = (int)nbin;
+  return (unsigned)(BH * nbin);
+}
+
+template <typename F>
+hipError_t launch(F kernel, const Params& p, int blocks_per_wg, int threads, int wgs, hipStream_t st) {
+  Params q = p;
+  const unsigned grid = set_bins(q, blocks_per_wg, wgs);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), 0, st, q);
+  return hipGetLastError();
 }
 
 template <int DP, bool SM, int W, int BN>
 hipError_t fwd_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_fwd_kernel<Elt, DP, W, BN, SM>), dim3(grid_of(p, W)), dim3(64 * W), 0, st, p);
-  return hipGetLastError();
+  auto k = rbf_fwd_kernel<Elt, DP, W, BN, SM>;
+  static const int wgs = wgs_per_cu(k, 64 * W);
+  return launch(k, p, W, 64 * W, wgs, st);
 }
 
 template <int DP, bool SM, int W, int QPW, int BN, bool EARLY = true>
 hipError_t dq_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_bwd_dq_kernel<Elt, DP, W, QPW, BN, SM, EARLY>), dim3(grid_of(p, W * QPW)), dim3(64 * W), 0,
-                     st, p);
-  return hipGetLastError();
+  auto k = rbf_bwd_dq_kernel<Elt, DP, W, QPW, BN, SM, EARLY>;
+  static const int wgs = wgs_per_cu(k, 64 * W);
+  return launch(k, p, W * QPW, 64 * W, wgs, st);
 }
 
 template <int DP, bool SM, int W, int KPW, int BM, bool EARLY = true, bool PIPE = false, bool PRIO = false>
 hipError_t dkdv_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_bwd_dkdv_kernel<Elt, DP, W, KPW, BM, SM, EARLY, PIPE, PRIO>),
-                     dim3(grid_of(p, W * KPW)), dim3(64 * W), 0, st, p);
-  return hipGetLastError();
+  auto k = rbf_bwd_dkdv_kernel<Elt, DP, W, KPW, BM, SM, EARLY, PIPE, PRIO>;
+  static const int wgs = wgs_per_cu(k, 64 * W);
+  return launch(k, p, W * KPW, 64 * W, wgs, st);
 }
 
 template <int DP, bool SM, int NP, int BM, bool SGB = false>
 hipError_t dkdv_pair_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_bwd_dkdv_pair_kernel<Elt, DP, NP, BM, SM, SGB>), dim3(grid_of(p, NP)), dim3(128 * NP), 0, st,
-                     p);
-  return hipGetLastError();
-}
-
-int env_choice(const char* name) {
-  const char* s = getenv(name);
-  return s ? atoi(s) : -1;
+  auto k = rbf_bwd_dkdv_pair_kernel<Elt, DP, NP, BM, SM, SGB>;
+  static const int wgs = wgs_per_cu(k, 128 * NP);
+  return launch(k, p, NP, 128 * NP, wgs, st);
 }
 
 // ---- defaults ------------------------------------------------------------
