@@ -1,0 +1,300 @@
+// Head-resident kernels for short sequences (16-bit elements).
+//
+// When a head's streamed operands fit in LDS (two (N, D) tensors and their
+// per-token scalars within ~150 KB: N <= 576 for D <= 64) and there are at
+// least as many heads as CUs, one work-group per head loads them once, then
+// every wave runs its own 32-token blocks against the resident tiles with no
+// further barriers.  Compared with the streaming kernels this removes the
+// per-tile barrier and the per-tile global-load latency from every wave's
+// chain, and the launch is a single round of equal work-groups.
+//
+// Waves take their blocks in snake order over the causal weights (heaviest
+// first), so each wave -- and each SIMD -- gets a near-equal share of the
+// head's 32x32 block pairs.
+#pragma once
+
+#include "rbf_attn_kernels.h"
+
+namespace rbf {
+
+// Chunk-major index of unit u: 16 consecutive units cover 4 tokens x 4
+// chunks, i.e. 64 contiguous bytes of each of 4 rows in global memory.
+template <int DP>
+__device__ inline void hr_unit(int u, int& row, int& ch) {
+  constexpr int CG = DP / 32;  // groups of 4 chunks per row
+  const int rest = u >> 4;
+  ch = 4 * (rest % CG) + (u & 3);
+  row = 4 * (rest / CG) + ((u >> 2) & 3);
+}
+
+// Loads rows [0, rows) -- tokens org + row -- of two (N, D) slices into
+// chunk-major LDS tiles of ROWS rows; tokens outside [0, N) and features
+// >= D are zero.  Every chunk of a thread is requested before the first is
+// stored.  The code is branch-free: with conditional stores here the compiler's
+// wait-count insertion no longer tells later LDS reads of other tiles apart
+// from outstanding LDS-DMA loads, and makes them wait for those loads.
+template <typename T, int ROWS, int DP, int NT>
+__device__ inline void hr_load2(const T* A, int64_t sa, T* sA, const T* B, int64_t sb, T* sB, int rows, int org,
+                                int N, int D, int tid) {
+  typedef typename Elem<T>::frag frag;
+  typedef CLayout<ROWS> L;
+  constexpr int PB = (ROWS * (DP / 8) + NT - 1) / NT;
+  const int units = rows * (DP / 8);
+  frag ra[PB], rb[PB];
+#pragma unroll
+  for (int j = 0; j < PB; ++j) {
+    const int u = tid + j * NT;
+    int row, ch;
+    hr_unit<DP>(u, row, ch);
+    const int tok = org + row;
+    const bool ok = u < units && tok >= 0 && tok < N && ch * 8 < D;
+    ra[j] = ok ? ld8<T>(A + (int64_t)tok * sa + ch * 8) : zero_frag<T>();
+    rb[j] = ok ? ld8<T>(B + (int64_t)tok * sb + ch * 8) : zero_frag<T>();
+  }
+  // Units past the tile store into the padding after chunk column 0 instead
+  // of branching around the store.
+#pragma unroll
+  for (int j = 0; j < PB; ++j) {
+    const int u = tid + j * NT;
+    int row, ch;
+    hr_unit<DP>(u, row, ch);
+    const int o = u < ROWS * (DP / 8) ? L::off(row, 8 * ch) : L::off(ROWS, 0);
+    st8<T>(sA + o, ra[j]);
+    st8<T>(sB + o, rb[j]);
+  }
+}
+
+// nrm[row] = -0.5 ||row||^2 of a resident chunk-major tile (fp32, from the
+// element-type values), -inf for padding rows (tokens outside [0, N)).
+template <typename T, int ROWS, int DP, int NT>
+__device__ inline void hr_neg_halfnorms(const T* sA, float* nrm, int rows, int org, int N, int tid) {
+  typedef CLayout<ROWS> L;
+  for (int r = tid; r < rows; r += NT) {
+    float s = 0.f;
+#pragma unroll
+    for (int ch = 0; ch < DP / 8; ++ch) s += sumsq8<T>(ld8<T>(sA + L::off(r, 8 * ch)));
+    const int tok = org + r;
+    nrm[r] = (tok >= 0 && tok < N) ? -0.5f * s : -__builtin_inff();
+  }
+}
+
+// Block index of the k-th block (k = 0, 1, ...) of `wave` out of W, or -1:
+// blocks ranked heaviest first (rank 0 = block nblk-1 when `reverse`, i.e.
+// when the weight rises with the block index), dealt in snake order.
+__device__ inline int hr_block(int k, int wave, int W, int nblk, bool reverse) {
+  const int rank = k * W + ((k & 1) ? W - 1 - wave : wave);
+  if (rank >= nblk) return -1;
+  return reverse ? nblk - 1 - rank : rank;
+}
+
+// ---------------------------------------------------------------------------
+// Forward, head-resident.  The work-group loads the head's K and V (and
+// -0.5||k||^2) into LDS once; wave w then computes the output of its query
+// blocks as rbf_fwd_group does per block (static softmax bound with the row
+// sum on the MFMA path; online max for fp16, or as a per-block rerun when a
+// row's sum leaves [2^-60, 2^100]), reading K rows and transposed V from the
+// resident tiles.
+//
+// Without a running max (static bound, non-softmax) the key loop is software
+// pipelined: iteration kb issues the S MFMAs of block kb+1 (K fragments and
+// norms read one block earlier) next to the exponentials of block kb, so the
+// MFMA and VALU work of one wave overlap.  Only the causal diagonal block
+// needs a mask; it is peeled off the loop.
+// ---------------------------------------------------------------------------
+template <typename T, int DP, int W, int NB, bool SOFTMAX>
+__global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
+  typedef Elem<T> E;
+  typedef typename E::frag frag;
+  static_assert(sizeof(T) == 2, "head-resident tiles are chunk-major 16-bit tiles");
+  constexpr int ROWS = 32 * NB, NT = 64 * W, KS = DP / 16, ND = DP / 32;
+  typedef CLayout<ROWS> L;
+  __shared__ __attribute__((aligned(16))) T sK[L::template size<DP>()];
+  __shared__ __attribute__((aligned(16))) T sV[L::template size<DP>()];
+  __shared__ __attribute__((aligned(16))) float sKn[ROWS];
+
+  if (p.nblk > NB) return;  // the host launches this kernel only for heads that fit
+  const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int N = p.N, D = p.D, org = p.org, nblk = p.nblk;
+  const bool causal = p.causal != 0;
+  const int npre = p.num_prefix;
+  const float c = p.c;
+  const int bh = blockIdx.x;
+  const int b = bh / p.H, hh = bh - b * p.H;
+  const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
+  const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
+  const T* V = reinterpret_cast<const T*>(p.v) + b * p.sv[0] + hh * p.sv[1];
+  T* O = reinterpret_cast<T*>(const_cast<void*>(p.o)) + b * p.so[0] + hh * p.so[1];
+
+  auto load_q = [&](int qb, frag* qf) {
+    const int qtok = org + 32 * qb + n;
+#pragma unroll
+    for (int t = 0; t < KS; ++t)
+      qf[t] = (qb >= 0 && qtok >= 0 && 16 * t + 8 * h < D) ? ld8<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h)
+                                                            : zero_frag<T>();
+  };
+  // The first query block's Q fragments are requested before the K/V load.
+  frag qf[KS];
+  int qb = hr_block(0, wave, W, nblk, causal);
+  load_q(qb, qf);
+
+  hr_load2<T, ROWS, DP, NT>(K, p.sk[2], sK, V, p.sv[2], sV, 32 * nblk, org, N, D, tid);
+  __syncthreads();
+  hr_neg_halfnorms<T, ROWS, DP, NT>(sK, sKn, 32 * nblk, org, N, tid);
+  __syncthreads();
+
+  auto load_k = [&](int kb, frag* kA) {
+#pragma unroll
+    for (int t = 0; t < KS; ++t) kA[t] = ld8<T>(sK + L::off(32 * kb + n, 16 * t + 8 * h));
+  };
+  auto load_vt = [&](int kb, frag (*vA)[2]) {
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) vA[d][t] = ld_trc<T, ROWS>(sV, 32 * kb + 16 * t, 32 * d, lane);
+  };
+  auto s_mma = [&](const frag* kA, f32x16_t s) {
+#pragma unroll
+    for (int t = 0; t < KS; ++t) s = E::mma(kA[t], qf[t], s);
+    return s;
+  };
+
+  const frag onesA = ones_row_frag<T>(n);
+  for (int k = 0; qb >= 0; ++k) {
+    // the next block's Q fragments are requested before this block's work
+    const int qb_next = hr_block(k + 1, wave, W, nblk, causal);
+    frag qf_next[KS];
+    load_q(qb_next, qf_next);
+    const int q0 = org + 32 * qb, qtok = q0 + n;
+    const bool qvalid = qtok >= 0;
+    const int jmax = last_key(qtok, N, causal, npre);
+    float qn2 = 0.f;
+#pragma unroll
+    for (int t = 0; t < KS; ++t) qn2 += sumsq8<T>(qf[t]);
+    qn2 = c * 0.5f * xhalf_sum(qn2);
+    // key blocks [0, kend) hold every key some query of the block sees
+    const int kend = causal ? min(nblk, ((max(q0 + 31, npre - 1) - org) >> 5) + 1) : nblk;
+
+    f32x16_t oacc[ND], lacc;
+    float m_run;
+    // P = exp2(c S - m) for one block, then O^T += V^T P^T and l += 1^T P^T
+    auto pv = [&](const f32x16_t& s, float moff, frag (*vA)[2]) {
+      frag pf[2];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pf[i >> 3][i & 7] = (T)fast_exp2(fmaf(s[i], c, -moff));
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int d = 0; d < ND; ++d) oacc[d] = E::mma(vA[d][t], pf[t], oacc[d]);
+        if constexpr (SOFTMAX) lacc = E::mma(onesA, pf[t], lacc);
+      }
+    };
+    auto init = [&](float m0) {
+#pragma unroll
+      for (int d = 0; d < ND; ++d) oacc[d] = zero16();
+      lacc = zero16();
+      m_run = m0;
+    };
+
+    // Online max with lazy rescaling (fp16 softmax, or the rerun of a block
+    // whose row sums left the static bound's range).
+    auto run_safe = [&]() {
+      init(SOFTMAX ? -__builtin_inff() : qn2);
+      for (int kb = 0; kb < kend; ++kb) {
+        const int k0 = org + 32 * kb;
+        frag kA[KS], vA[ND][2];
+        load_k(kb, kA);
+        f32x16_t s = s_mma(kA, ld_rows16(sKn + 32 * kb, h));
+        load_vt(kb, vA);
+        if (!blk_nomask(q0, k0, causal, npre)) mask_key_rows(s, k0, h, jmax);
+        if constexpr (SOFTMAX) {
+          const float mt = xhalf_max(tree_max16(s)) * c;
+          if (__any(mt > m_run + kTau)) {
+            const float mnew = fmaxf(m_run, mt);
+            const float alpha = (mnew == -__builtin_inff()) ? 1.f : fast_exp2(m_run - mnew);
+#pragma unroll
+            for (int d = 0; d < ND; ++d) oacc[d] *= alpha;
+            lacc *= alpha;
+            m_run = mnew;
+          }
+        }
+        pv(s, m_run == -__builtin_inff() ? 0.f : m_run, vA);
+      }
+    };
+
+    // Fixed offset (static bound or non-softmax), software pipelined.  With
+    // num_prefix == 0 the blocks before the last need no mask (causal: the
+    // last block is the diagonal one; not causal: padding keys are -inf
+    // through their norms).
+    auto run_fixed = [&]() {
+      init(SOFTMAX ? qn2 - kBoundMargin : qn2);
+      const float moff = m_run;
+      const int last = kend - 1;
+      frag kA[KS], vA[ND][2];
+      load_k(0, kA);
+      f32x16_t s = s_mma(kA, ld_rows16(sKn, h));
+      load_k(min(1, last), kA);
+      f32x16_t nrm = ld_rows16(sKn + 32 * min(1, last), h);
+      for (int kb = 0; kb < last; ++kb) {
+        load_vt(kb, vA);
+        const f32x16_t sn = s_mma(kA, nrm);  // S of block kb + 1
+        const int k2 = min(kb + 2, last);
+        load_k(k2, kA);
+        nrm = ld_rows16(sKn + 32 * k2, h);
+        pv(s, moff, vA);
+        s = sn;
+      }
+      load_vt(last, vA);
+      if (causal) mask_key_rows(s, org + 32 * last, h, jmax);
+      pv(s, moff, vA);
+    };
+
+    constexpr bool STATIC = SOFTMAX && !std::is_same<T, _Float16>::value;
+    if (!(SOFTMAX && !STATIC) && npre == 0) {
+      run_fixed();
+    } else if constexpr (SOFTMAX && !STATIC) {
+      run_safe();
+    } else {
+      // fixed offset with a num_prefix mask: the generic loop at the fixed offset
+      init(SOFTMAX ? qn2 - kBoundMargin : qn2);
+      for (int kb = 0; kb < kend; ++kb) {
+        const int k0 = org + 32 * kb;
+        frag kA[KS], vA[ND][2];
+        load_k(kb, kA);
+        f32x16_t s = s_mma(kA, ld_rows16(sKn + 32 * kb, h));
+        load_vt(kb, vA);
+        if (!blk_nomask(q0, k0, causal, npre)) mask_key_rows(s, k0, h, jmax);
+        pv(s, m_run, vA);
+      }
+    }
+    if constexpr (STATIC) {
+      const float l = xhalf_sum(lacc[0]);
+      const bool bad = qvalid && !(l >= kSumLow && l <= kSumHigh);
+      if (__any(bad)) run_safe();
+    }
+
+    const float lsum = SOFTMAX ? xhalf_sum(lacc[0]) : 1.f;
+    const float inv = SOFTMAX ? 1.f / lsum : 1.f;
+    if (qvalid) {
+      T* orow = O + (int64_t)qtok * p.so[2];
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int dd = 32 * d + 8 * g + 4 * h;
+          if (dd < D) {
+            float v4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v4[e] = oacc[d][4 * g + e] * inv;
+            st4f<T>(orow + dd, v4);
+          }
+        }
+      if (SOFTMAX && h == 0) p.lse[(int64_t)bh * N + qtok] = m_run + __log2f(lsum);
+    }
+    qb = qb_next;
+#pragma unroll
+    for (int t = 0; t < KS; ++t) qf[t] = qf_next[t];
+  }
+}
+
+}  // namespace rbf

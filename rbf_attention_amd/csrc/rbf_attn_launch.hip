@@ -9,6 +9,7 @@
 // (an index into the candidate lists below) for tuning sweeps.
 #include <stdlib.h>
 
+#include "rbf_attn_hr_kernels.h"
 #include "rbf_attn_kernels.h"
 #include "rbf_attn_launch.h"
 #include "rbf_decode_kernels.h"
@@ -82,6 +83,25 @@ hipError_t launch(F kernel, const Params& p, int blocks_per_wg, int threads, int
   return hipGetLastError();
 }
 
+template <int DP, bool SM, int W, int NB>
+hipError_t fwd_hr_cfg(const Params& p, hipStream_t st) {
+  hipLaunchKernelGGL((rbf_fwd_hr_kernel<Elt, DP, W, NB, SM>), dim3((unsigned)((long long)p.B * p.H)), dim3(64 * W), 0,
+                     st, p);
+  return hipGetLastError();
+}
+
+// Head-resident kernels (16-bit): the head's nblk blocks fit the kernel's LDS
+// tiles (nb_max blocks) and there are at least as many heads as CUs, so one
+// work-group per head fills the GPU.  RBF_ATTN_HR=0 disables them, =1 uses
+// them whenever the head fits.
+bool use_hr(const Params& p, int nb_max) {
+  static const int forced = env_choice("RBF_ATTN_HR");
+  if (kIsF32 || forced == 0 || p.nblk > nb_max) return false;
+  if (forced > 0) return true;
+  return (long long)p.B * p.H >= cu_count();
+}
+constexpr int kHrBlocks64 = 18;  // D <= 64: N <= 576
+
 template <int DP, bool SM, int W, int BN>
 hipError_t fwd_cfg(const Params& p, hipStream_t st) {
   auto k = rbf_fwd_kernel<Elt, DP, W, BN, SM>;
@@ -118,6 +138,9 @@ constexpr int kLongSeq = 2048;
 
 template <int DP, bool SM>
 hipError_t fwd_default(const Params& p, hipStream_t st) {
+  if constexpr (!kIsF32 && DP == 64) {
+    if (use_hr(p, kHrBlocks64)) return fwd_hr_cfg<DP, SM, 12, kHrBlocks64>(p, st);
+  }
   if constexpr (kIsF32) return fwd_cfg<DP, SM, 4, 32>(p, st);
   else if constexpr (DP <= 64)
     return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 128>(p, st) : fwd_cfg<DP, SM, 4, 64>(p, st);
@@ -153,6 +176,15 @@ hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
     case 3: return fwd_cfg<DP, SM, 4, 128>(p, st);
     case 4: return fwd_cfg<DP, SM, 2, 64>(p, st);
     case 5: return fwd_cfg<DP, SM, 4, 32>(p, st);
+    case 10:
+      if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return fwd_hr_cfg<DP, SM, 8, kHrBlocks64>(p, st); }
+      break;
+    case 11:
+      if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return fwd_hr_cfg<DP, SM, 12, kHrBlocks64>(p, st); }
+      break;
+    case 12:
+      if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return fwd_hr_cfg<DP, SM, 16, kHrBlocks64>(p, st); }
+      break;
     default: break;
   }
 #endif
