@@ -239,7 +239,7 @@ def decode_bench(dev, iters: int):
         "dtype": "bf16",
         "config": dict(c, workload="decode_kv16k_bf16", softmax=True, gamma=gamma),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_GBS, 4), "traffic": measured_traffic("decode_kv16k_bf16", "decode")},
     }
 
 

@@ -552,8 +552,17 @@ __device__ inline void decode_wg(int nbin, int hchunk, int& bh, int& bin) {
 // with fewer bins the host picks R so that all work-groups run at once and
 // the snake order gives them near-equal causal work.  The bin's groups run
 // back to back, separated by a barrier (they reuse the LDS tiles).
-template <typename F>
+// BIN = false compiles the one-group-per-work-group form only (no loop
+// around the body: the loop costs the long-sequence kernels registers and
+// speed).
+template <bool BIN, typename F>
 __device__ __forceinline__ void for_each_group(const Params& p, int ngrp, bool reverse, F&& f) {
+  if constexpr (!BIN) {
+    int bh, rank;
+    decode_wg(ngrp, p.hchunk, bh, rank);
+    f(bh, reverse ? ngrp - 1 - rank : rank);
+    return;
+  }
   const int nbin = (p.nbin > 0 && p.nbin < ngrp) ? p.nbin : ngrp;
   int bh, bin;
   decode_wg(nbin, p.hchunk, bh, bin);
@@ -835,12 +844,13 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
   if (SOFTMAX && h == 0) p.lse[(int64_t)bh * N + qtok] = m_run + __log2f(lsum);
 }
 
-// WPE > 0 asks the compiler for at least WPE waves per SIMD (register
-// budget 512 / WPE): the 16-bit D <= 64 forward keeps three, as it has without
-// the bin loop around its body.
-template <typename T, int DP, int W, int BN, bool SOFTMAX, int WPE = (sizeof(T) == 2 && DP <= 64) ? 3 : 1>
+// WPE asks the compiler for at least WPE waves per SIMD (register budget
+// 512 / WPE): the binned 16-bit D <= 64 forward keeps three, as it has
+// without the bin loop around its body.
+template <typename T, int DP, int W, int BN, bool SOFTMAX, bool BIN = false,
+          int WPE = (BIN && sizeof(T) == 2 && DP <= 64) ? 3 : 1>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void rbf_fwd_kernel(const Params p) {
-  for_each_group(p, (p.nblk + W - 1) / W, p.causal != 0,
+  for_each_group<BIN>(p, (p.nblk + W - 1) / W, p.causal != 0,
                  [&](int bh, int grp) { rbf_fwd_group<T, DP, W, BN, SOFTMAX>(p, bh, grp); });
 }
 
@@ -1070,9 +1080,9 @@ __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int gr
   }
 }
 
-template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX, bool EARLY = true>
+template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX, bool EARLY = true, bool BIN = false>
 __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
-  for_each_group(p, (p.nblk + W * QPW - 1) / (W * QPW), p.causal != 0,
+  for_each_group<BIN>(p, (p.nblk + W * QPW - 1) / (W * QPW), p.causal != 0,
                  [&](int bh, int grp) { rbf_bwd_dq_group<T, DP, W, QPW, BN, SOFTMAX, EARLY>(p, bh, grp); });
 }
 
@@ -1378,9 +1388,9 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
 }
 
 template <typename T, int DP, int W, int KPW, int BM, bool SOFTMAX, bool EARLY = true, bool PIPE = false,
-          bool PRIO = false>
+          bool PRIO = false, bool BIN = false>
 __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
-  for_each_group(p, (p.nblk + W * KPW - 1) / (W * KPW), false,
+  for_each_group<BIN>(p, (p.nblk + W * KPW - 1) / (W * KPW), false,
                  [&](int bh, int grp) { rbf_bwd_dkdv_group<T, DP, W, KPW, BM, SOFTMAX, EARLY, PIPE, PRIO>(p, bh, grp); });
 }
 
@@ -1609,9 +1619,9 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
     }
 }
 
-template <typename T, int DP, int NP, int BM, bool SOFTMAX, bool SGB = false>
+template <typename T, int DP, int NP, int BM, bool SOFTMAX, bool SGB = false, bool BIN = false>
 __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Params p) {
-  for_each_group(p, (p.nblk + NP - 1) / NP, false,
+  for_each_group<BIN>(p, (p.nblk + NP - 1) / NP, false,
                  [&](int bh, int grp) { rbf_bwd_dkdv_pair_group<T, DP, NP, BM, SOFTMAX, SGB>(p, bh, grp); });
 }
 

@@ -60,14 +60,20 @@ int wgs_per_cu(F kernel, int threads) {
 // (`wgs` per CU), so that the launch runs in one round of near-equal
 // work-groups instead of a heavy round followed by a tail of light, short
 // ones.  RBF_ATTN_NBIN=n forces n bins per head (0: one group per bin).
-unsigned set_bins(Params& p, int blocks_per_wg, int wgs) {
+unsigned set_bins(Params& p, int blocks_per_wg, int wgs, bool binned) {
   const int ngrp = (p.nblk + blocks_per_wg - 1) / blocks_per_wg;
   const long long BH = (long long)p.B * p.H;
   static const int forced = env_choice("RBF_ATTN_NBIN");
   long long nbin = ngrp;
-  if (forced > 0) {
+  if (!binned) {
+    // kernel compiled without the bin loop
+  } else if (forced > 0) {
     nbin = forced < ngrp ? forced : ngrp;
-  } else if (forced < 0 && BH > 0) {
+  } else if (forced < 0 && BH > 0 && (BH + 7) / 8 * 2LL * p.N * p.D * (long long)sizeof(Elt) <= (16LL << 20)) {
+    // Only when the streamed operands (K and V, or Q and dO) of all heads of
+    // an XCD stay within about its L2 size: the bins of all heads run at
+    // once, so longer heads would stream them from HBM instead of sharing
+    // them in L2 head by head.
     const long long slots = (long long)cu_count() * wgs;
     if (BH * ngrp > slots) nbin = slots / BH < 1 ? 1 : (slots / BH < ngrp ? slots / BH : ngrp);
   }
@@ -76,9 +82,9 @@ unsigned set_bins(Params& p, int blocks_per_wg, int wgs) {
 }
 
 template <typename F>
-hipError_t launch(F kernel, const Params& p, int blocks_per_wg, int threads, int wgs, hipStream_t st) {
+hipError_t launch(F kernel, const Params& p, int blocks_per_wg, int threads, int wgs, bool binned, hipStream_t st) {
   Params q = p;
-  const unsigned grid = set_bins(q, blocks_per_wg, wgs);
+  const unsigned grid = set_bins(q, blocks_per_wg, wgs, binned);
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), 0, st, q);
   return hipGetLastError();
 }
@@ -102,36 +108,39 @@ bool use_hr(const Params& p, int nb_max) {
 }
 constexpr int kHrBlocks64 = 18;  // D <= 64: N <= 576
 
-template <int DP, bool SM, int W, int BN>
+template <int DP, bool SM, int W, int BN, bool BIN = false>
 hipError_t fwd_cfg(const Params& p, hipStream_t st) {
-  auto k = rbf_fwd_kernel<Elt, DP, W, BN, SM>;
+  auto k = rbf_fwd_kernel<Elt, DP, W, BN, SM, BIN>;
   static const int wgs = wgs_per_cu(k, 64 * W);
-  return launch(k, p, W, 64 * W, wgs, st);
+  return launch(k, p, W, 64 * W, wgs, BIN, st);
 }
 
-template <int DP, bool SM, int W, int QPW, int BN, bool EARLY = true>
+template <int DP, bool SM, int W, int QPW, int BN, bool EARLY = true, bool BIN = false>
 hipError_t dq_cfg(const Params& p, hipStream_t st) {
-  auto k = rbf_bwd_dq_kernel<Elt, DP, W, QPW, BN, SM, EARLY>;
+  auto k = rbf_bwd_dq_kernel<Elt, DP, W, QPW, BN, SM, EARLY, BIN>;
   static const int wgs = wgs_per_cu(k, 64 * W);
-  return launch(k, p, W * QPW, 64 * W, wgs, st);
+  return launch(k, p, W * QPW, 64 * W, wgs, BIN, st);
 }
 
-template <int DP, bool SM, int W, int KPW, int BM, bool EARLY = true, bool PIPE = false, bool PRIO = false>
+template <int DP, bool SM, int W, int KPW, int BM, bool EARLY = true, bool PIPE = false, bool PRIO = false,
+          bool BIN = false>
 hipError_t dkdv_cfg(const Params& p, hipStream_t st) {
-  auto k = rbf_bwd_dkdv_kernel<Elt, DP, W, KPW, BM, SM, EARLY, PIPE, PRIO>;
+  auto k = rbf_bwd_dkdv_kernel<Elt, DP, W, KPW, BM, SM, EARLY, PIPE, PRIO, BIN>;
   static const int wgs = wgs_per_cu(k, 64 * W);
-  return launch(k, p, W * KPW, 64 * W, wgs, st);
+  return launch(k, p, W * KPW, 64 * W, wgs, BIN, st);
 }
 
-template <int DP, bool SM, int NP, int BM, bool SGB = false>
+template <int DP, bool SM, int NP, int BM, bool SGB = false, bool BIN = false>
 hipError_t dkdv_pair_cfg(const Params& p, hipStream_t st) {
-  auto k = rbf_bwd_dkdv_pair_kernel<Elt, DP, NP, BM, SM, SGB>;
+  auto k = rbf_bwd_dkdv_pair_kernel<Elt, DP, NP, BM, SM, SGB, BIN>;
   static const int wgs = wgs_per_cu(k, 128 * NP);
-  return launch(k, p, NP, 128 * NP, wgs, st);
+  return launch(k, p, NP, 128 * NP, wgs, BIN, st);
 }
 
 // ---- defaults ------------------------------------------------------------
 // Chosen from measured sweeps on MI355X (N = 516 and N = 8196, D = 64 / 128).
+// Short heads use the binned kernels (see set_bins), long heads the
+// one-group-per-work-group form.
 // The forward switches to 8-wave work-groups over longer key tiles once a
 // head has enough tokens to keep them busy.
 constexpr int kLongSeq = 2048;
@@ -143,25 +152,28 @@ hipError_t fwd_default(const Params& p, hipStream_t st) {
   }
   if constexpr (kIsF32) return fwd_cfg<DP, SM, 4, 32>(p, st);
   else if constexpr (DP <= 64)
-    return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 128>(p, st) : fwd_cfg<DP, SM, 4, 64>(p, st);
+    return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 128>(p, st) : fwd_cfg<DP, SM, 4, 64, true>(p, st);
   else
-    return fwd_cfg<DP, SM, 8, 64>(p, st);
+    return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 64>(p, st) : fwd_cfg<DP, SM, 8, 64, true>(p, st);
 }
 
 template <int DP, bool SM>
 hipError_t dq_default(const Params& p, hipStream_t st) {
   if constexpr (kIsF32) return dq_cfg<DP, SM, 4, 1, 32>(p, st);
-  else if constexpr (DP <= 64) return dq_cfg<DP, SM, 4, 1, 128>(p, st);
-  else return dq_cfg<DP, SM, 8, 1, 32>(p, st);
+  else if constexpr (DP <= 64)
+    return p.N >= kLongSeq ? dq_cfg<DP, SM, 4, 1, 128>(p, st) : dq_cfg<DP, SM, 4, 1, 128, true, true>(p, st);
+  else
+    return p.N >= kLongSeq ? dq_cfg<DP, SM, 8, 1, 32>(p, st) : dq_cfg<DP, SM, 8, 1, 32, true, true>(p, st);
 }
 
 template <int DP, bool SM>
 hipError_t dkdv_default(const Params& p, hipStream_t st) {
   if constexpr (kIsF32) return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
   else if constexpr (DP <= 64)
-    return p.N >= kLongSeq ? dkdv_cfg<DP, SM, 8, 1, 128>(p, st) : dkdv_cfg<DP, SM, 4, 1, 128, false>(p, st);
+    return p.N >= kLongSeq ? dkdv_cfg<DP, SM, 8, 1, 128>(p, st)
+                           : dkdv_cfg<DP, SM, 4, 1, 128, false, false, false, true>(p, st);
   else
-    return p.N >= kLongSeq ? dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st) : dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
+    return p.N >= kLongSeq ? dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st) : dkdv_pair_cfg<DP, SM, 2, 64, false, true>(p, st);
 }
 
 // ---- tuning candidates (bf16, 32 < D <= 64) ------------------------------
