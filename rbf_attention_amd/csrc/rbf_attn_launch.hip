@@ -60,6 +60,16 @@ int wgs_per_cu(F kernel, int threads) {
 // (`wgs` per CU), so that the launch runs in one round of near-equal
 // work-groups instead of a heavy round followed by a tail of light, short
 // ones.  RBF_ATTN_NBIN=n forces n bins per head (0: one group per bin).
+// Whether the binned kernels suit this problem: the streamed operands (K and
+// V, or Q and dO) of all heads of an XCD stay within about its L2 size.  The
+// bins of all heads run at once, so longer heads would stream them from HBM
+// instead of sharing them in L2 head by head (the one-group form runs a
+// head's groups together, heaviest first).
+bool bins_fit(const Params& p) {
+  const long long BH = (long long)p.B * p.H;
+  return (BH + 7) / 8 * 2LL * p.N * p.D * (long long)sizeof(Elt) <= (16LL << 20);
+}
+
 unsigned set_bins(Params& p, int blocks_per_wg, int wgs, bool binned) {
   const int ngrp = (p.nblk + blocks_per_wg - 1) / blocks_per_wg;
   const long long BH = (long long)p.B * p.H;
@@ -69,11 +79,7 @@ unsigned set_bins(Params& p, int blocks_per_wg, int wgs, bool binned) {
     // kernel compiled without the bin loop
   } else if (forced > 0) {
     nbin = forced < ngrp ? forced : ngrp;
-  } else if (forced < 0 && BH > 0 && (BH + 7) / 8 * 2LL * p.N * p.D * (long long)sizeof(Elt) <= (16LL << 20)) {
-    // Only when the streamed operands (K and V, or Q and dO) of all heads of
-    // an XCD stay within about its L2 size: the bins of all heads run at
-    // once, so longer heads would stream them from HBM instead of sharing
-    // them in L2 head by head.
+  } else if (forced < 0 && BH > 0) {
     const long long slots = (long long)cu_count() * wgs;
     if (BH * ngrp > slots) nbin = slots / BH < 1 ? 1 : (slots / BH < ngrp ? slots / BH : ngrp);
   }
@@ -139,8 +145,8 @@ hipError_t dkdv_pair_cfg(const Params& p, hipStream_t st) {
 
 // ---- defaults ------------------------------------------------------------
 // Chosen from measured sweeps on MI355X (N = 516 and N = 8196, D = 64 / 128).
-// Short heads use the binned kernels (see set_bins), long heads the
-// one-group-per-work-group form.
+// Heads whose operands share L2 use the binned kernels (bins_fit,
+// set_bins), others the one-group-per-work-group form.
 // The forward switches to 8-wave work-groups over longer key tiles once a
 // head has enough tokens to keep them busy.
 constexpr int kLongSeq = 2048;
@@ -151,29 +157,36 @@ hipError_t fwd_default(const Params& p, hipStream_t st) {
     if (use_hr(p, kHrBlocks64)) return fwd_hr_cfg<DP, SM, 12, kHrBlocks64>(p, st);
   }
   if constexpr (kIsF32) return fwd_cfg<DP, SM, 4, 32>(p, st);
-  else if constexpr (DP <= 64)
-    return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 128>(p, st) : fwd_cfg<DP, SM, 4, 64, true>(p, st);
-  else
-    return p.N >= kLongSeq ? fwd_cfg<DP, SM, 8, 64>(p, st) : fwd_cfg<DP, SM, 8, 64, true>(p, st);
+  else if constexpr (DP <= 64) {
+    if (p.N >= kLongSeq) return bins_fit(p) ? fwd_cfg<DP, SM, 8, 128, true>(p, st) : fwd_cfg<DP, SM, 8, 128>(p, st);
+    return bins_fit(p) ? fwd_cfg<DP, SM, 4, 64, true>(p, st) : fwd_cfg<DP, SM, 4, 64>(p, st);
+  } else {
+    return bins_fit(p) ? fwd_cfg<DP, SM, 8, 64, true>(p, st) : fwd_cfg<DP, SM, 8, 64>(p, st);
+  }
 }
 
 template <int DP, bool SM>
 hipError_t dq_default(const Params& p, hipStream_t st) {
   if constexpr (kIsF32) return dq_cfg<DP, SM, 4, 1, 32>(p, st);
   else if constexpr (DP <= 64)
-    return p.N >= kLongSeq ? dq_cfg<DP, SM, 4, 1, 128>(p, st) : dq_cfg<DP, SM, 4, 1, 128, true, true>(p, st);
+    return bins_fit(p) ? dq_cfg<DP, SM, 4, 1, 128, true, true>(p, st) : dq_cfg<DP, SM, 4, 1, 128>(p, st);
   else
-    return p.N >= kLongSeq ? dq_cfg<DP, SM, 8, 1, 32>(p, st) : dq_cfg<DP, SM, 8, 1, 32, true, true>(p, st);
+    return bins_fit(p) ? dq_cfg<DP, SM, 8, 1, 32, true, true>(p, st) : dq_cfg<DP, SM, 8, 1, 32>(p, st);
 }
 
 template <int DP, bool SM>
 hipError_t dkdv_default(const Params& p, hipStream_t st) {
   if constexpr (kIsF32) return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
-  else if constexpr (DP <= 64)
-    return p.N >= kLongSeq ? dkdv_cfg<DP, SM, 8, 1, 128>(p, st)
-                           : dkdv_cfg<DP, SM, 4, 1, 128, false, false, false, true>(p, st);
-  else
-    return p.N >= kLongSeq ? dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st) : dkdv_pair_cfg<DP, SM, 2, 64, false, true>(p, st);
+  else if constexpr (DP <= 64) {
+    if (p.N >= kLongSeq)
+      return bins_fit(p) ? dkdv_cfg<DP, SM, 8, 1, 128, true, false, false, true>(p, st) : dkdv_cfg<DP, SM, 8, 1, 128>(p, st);
+    return bins_fit(p) ? dkdv_cfg<DP, SM, 4, 1, 128, false, false, false, true>(p, st)
+                       : dkdv_cfg<DP, SM, 4, 1, 128, false>(p, st);
+  } else {
+    // the long-sequence paired kernel measured slower with the bin loop
+    if (p.N >= kLongSeq) return dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st);
+    return bins_fit(p) ? dkdv_pair_cfg<DP, SM, 2, 64, false, true>(p, st) : dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
+  }
 }
 
 // ---- tuning candidates (bf16, 32 < D <= 64) ------------------------------
