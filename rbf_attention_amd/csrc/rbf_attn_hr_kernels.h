@@ -297,4 +297,167 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// dK / dV, head-resident.  The work-group holds the head's Q and dO
+// (chunk-major) and the per-query offsets -L/c (non-softmax: -0.5||q||^2)
+// and -Delta in LDS; wave w takes key blocks in snake order over the causal
+// weights (key block j is seen by the query blocks from j on, so block 0 is
+// the heaviest) and, per key block, runs the query blocks that see it exactly
+// as rbf_bwd_dkdv_group does per 32x32 block:
+//   S = Q K^T (init -L/c), P = exp2(c S - c 0.5||k||^2), dP = dO V^T (init
+//   -Delta), dS = P dP, dV^T += dO^T P, dK^T += Q^T dS, colsum += dS,
+// with K and V in registers and no barrier after the load.
+// ---------------------------------------------------------------------------
+template <typename T, int DP, int W, int NB, bool SOFTMAX>
+__global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p) {
+  typedef Elem<T> E;
+  typedef typename E::frag frag;
+  static_assert(sizeof(T) == 2, "head-resident tiles are chunk-major 16-bit tiles");
+  constexpr int ROWS = 32 * NB, NT = 64 * W, KS = DP / 16, ND = DP / 32;
+  typedef CLayout<ROWS> L;
+  __shared__ __attribute__((aligned(16))) T sQ[L::template size<DP>()];
+  __shared__ __attribute__((aligned(16))) T sD[L::template size<DP>()];
+  __shared__ __attribute__((aligned(16))) float sOff[ROWS];
+  __shared__ __attribute__((aligned(16))) float sDel[ROWS];
+
+  if (p.nblk > NB) return;  // the host launches this kernel only for heads that fit
+  const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int N = p.N, D = p.D, org = p.org, nblk = p.nblk;
+  const bool causal = p.causal != 0;
+  const int npre = p.num_prefix;
+  const float c = p.c;
+  const float inv_c = 1.f / c;
+  const int bh = blockIdx.x;
+  const int b = bh / p.H, hh = bh - b * p.H;
+  const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
+  const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
+  const T* V = reinterpret_cast<const T*>(p.v) + b * p.sv[0] + hh * p.sv[1];
+  const T* dO = reinterpret_cast<const T*>(p.dout) + b * p.sdo[0] + hh * p.sdo[1];
+  T* dK = reinterpret_cast<T*>(p.dk) + b * p.sdk[0] + hh * p.sdk[1];
+  T* dV = reinterpret_cast<T*>(p.dv) + b * p.sdv[0] + hh * p.sdv[1];
+  const float* offg = p.lse + (int64_t)bh * N;
+  const float* delg = SOFTMAX ? p.delta + (int64_t)bh * N : nullptr;
+
+  // K, V and -c 0.5||k||^2 of one key block, straight to registers.
+  frag kf[KS], vf[KS];
+  float nckn = 0.f;
+  auto load_kv = [&](int kb) {
+    const int ktok = org + 32 * kb + n;
+    float ss = 0.f;
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      const bool ok = kb >= 0 && ktok >= 0 && 16 * t + 8 * h < D;
+      kf[t] = ok ? ld8<T>(K + (int64_t)ktok * p.sk[2] + 16 * t + 8 * h) : zero_frag<T>();
+      vf[t] = ok ? ld8<T>(V + (int64_t)ktok * p.sv[2] + 16 * t + 8 * h) : zero_frag<T>();
+      ss += sumsq8<T>(kf[t]);
+    }
+    nckn = -c * 0.5f * xhalf_sum(ss);
+  };
+  int kb = hr_block(0, wave, W, nblk, false);
+  load_kv(kb);
+
+  hr_load2<T, ROWS, DP, NT>(Q, p.sq[2], sQ, dO, p.sdo[2], sD, 32 * nblk, org, N, D, tid);
+  for (int r = tid; r < 32 * nblk; r += NT) {
+    const int tok = org + r;
+    const bool ok = tok >= 0 && tok < N;
+    sOff[r] = ok ? -offg[tok] * inv_c : -__builtin_inff();  // padding queries: P = 0
+    sDel[r] = (SOFTMAX && ok) ? -delg[tok] : 0.f;
+  }
+  __syncthreads();
+
+  const float g2 = 2.f * p.gamma;
+  for (int k = 0; kb >= 0; ++k) {
+    const int k0 = org + 32 * kb, ktok = k0 + n;
+    const int ilo = first_query(ktok, causal, npre);
+    // query blocks [qb0, nblk) hold every query that sees some key of the block
+    const int qlo = causal ? (max(k0, 0) < npre ? 0 : max(k0, 0)) : 0;
+    const int qb0 = max(0, (qlo - org) >> 5);
+
+    f32x16_t dkacc[ND], dvacc[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+      dkacc[d] = zero16();
+      dvacc[d] = zero16();
+    }
+    float csum = 0.f;
+    // Q and dO row fragments of the next query block are read while this
+    // block's products and exponentials run.
+    frag qA[KS], dA[KS];
+    auto load_rows = [&](int qb) {
+#pragma unroll
+      for (int t = 0; t < KS; ++t) {
+        qA[t] = ld8<T>(sQ + L::off(32 * qb + n, 16 * t + 8 * h));
+        dA[t] = ld8<T>(sD + L::off(32 * qb + n, 16 * t + 8 * h));
+      }
+    };
+    load_rows(qb0);
+    for (int qb = qb0; qb < nblk; ++qb) {
+      const int q0 = org + 32 * qb;
+      f32x16_t s = ld_rows16(sOff + 32 * qb, h);
+      f32x16_t dp = SOFTMAX ? ld_rows16(sDel + 32 * qb, h) : zero16();
+#pragma unroll
+      for (int t = 0; t < KS; ++t) {
+        s = E::mma(qA[t], kf[t], s);
+        dp = E::mma(dA[t], vf[t], dp);
+      }
+      load_rows(min(qb + 1, nblk - 1));
+      // dO^T and Q^T fragments are read while the S / dP MFMAs run.
+      frag dtA[ND][2], qtA[ND][2];
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          dtA[d][t] = ld_trc<T, ROWS>(sD, 32 * qb + 16 * t, 32 * d, lane);
+          qtA[d][t] = ld_trc<T, ROWS>(sQ, 32 * qb + 16 * t, 32 * d, lane);
+        }
+      if (!blk_nomask(q0, k0, causal, npre)) mask_query_rows(s, q0, h, ilo);
+      frag pf[2], sf[2];
+      float ds[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float pv = fast_exp2(fmaf(s[i], c, nckn));
+        ds[i] = pv * dp[i];
+        pf[i >> 3][i & 7] = (T)pv;
+        sf[i >> 3][i & 7] = (T)ds[i];
+      }
+      csum += tree_sum16(ds);
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          dvacc[d] = E::mma(dtA[d][t], pf[t], dvacc[d]);
+          dkacc[d] = E::mma(qtA[d][t], sf[t], dkacc[d]);
+        }
+    }
+
+    const float cs = xhalf_sum(csum);
+    const int kb_next = hr_block(k + 1, wave, W, nblk, false);
+    if (ktok >= 0) {
+      T* dkrow = dK + (int64_t)ktok * p.sdk[2];
+      T* dvrow = dV + (int64_t)ktok * p.sdv[2];
+      const T* krow = K + (int64_t)ktok * p.sk[2];
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int dd = 32 * d + 8 * g + 4 * h;
+          if (dd < D) {
+            float k4[4], a4[4], b4[4];
+            ld4f<T>(krow + dd, k4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              a4[e] = g2 * (dkacc[d][4 * g + e] - cs * k4[e]);
+              b4[e] = dvacc[d][4 * g + e];
+            }
+            st4f<T>(dkrow + dd, a4);
+            st4f<T>(dvrow + dd, b4);
+          }
+        }
+    }
+    kb = kb_next;
+    if (kb >= 0) load_kv(kb);
+  }
+}
+
 }  // namespace rbf

@@ -102,6 +102,13 @@ hipError_t fwd_hr_cfg(const Params& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int DP, bool SM, int W, int NB>
+hipError_t dkdv_hr_cfg(const Params& p, hipStream_t st) {
+  hipLaunchKernelGGL((rbf_bwd_dkdv_hr_kernel<Elt, DP, W, NB, SM>), dim3((unsigned)((long long)p.B * p.H)),
+                     dim3(64 * W), 0, st, p);
+  return hipGetLastError();
+}
+
 // Head-resident kernels (16-bit): the head's nblk blocks fit the kernel's LDS
 // tiles (nb_max blocks) and there are at least as many heads as CUs, so one
 // work-group per head fills the GPU.  RBF_ATTN_HR=0 disables them, =1 uses
@@ -176,6 +183,9 @@ hipError_t dq_default(const Params& p, hipStream_t st) {
 
 template <int DP, bool SM>
 hipError_t dkdv_default(const Params& p, hipStream_t st) {
+  if constexpr (!kIsF32 && DP == 64) {
+    if (use_hr(p, kHrBlocks64)) return dkdv_hr_cfg<DP, SM, 8, kHrBlocks64>(p, st);
+  }
   if constexpr (kIsF32) return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
   else if constexpr (DP <= 64) {
     if (p.N >= kLongSeq)
@@ -206,9 +216,6 @@ hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
       break;
     case 11:
       if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return fwd_hr_cfg<DP, SM, 12, kHrBlocks64>(p, st); }
-      break;
-    case 12:
-      if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return fwd_hr_cfg<DP, SM, 16, kHrBlocks64>(p, st); }
       break;
     default: break;
   }
