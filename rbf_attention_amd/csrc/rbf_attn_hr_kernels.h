@@ -460,4 +460,164 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
   }
 }
 
+// ---------------------------------------------------------------------------
+// dQ (and Delta), head-resident.  The work-group holds the head's K, V and
+// -0.5||k||^2 in LDS; wave w takes query blocks in snake order over the
+// causal weights and, per query block, computes Delta = rowsum(O dO) (or the
+// non-softmax norm offset) as rbf_bwd_dq_group does, then runs the key
+// blocks the block sees:
+//   S^T = K Q^T (init -0.5||k||^2), P = exp2(c S^T - L), dP^T = V dO^T
+//   (init -Delta), dS = P dP^T, dQ^T += K^T dS^T,
+// with the next key block's K and V rows read one block ahead and no
+// barrier after the load.
+// ---------------------------------------------------------------------------
+template <typename T, int DP, int W, int NB, bool SOFTMAX>
+__global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
+  typedef Elem<T> E;
+  typedef typename E::frag frag;
+  static_assert(sizeof(T) == 2, "head-resident tiles are chunk-major 16-bit tiles");
+  constexpr int ROWS = 32 * NB, NT = 64 * W, KS = DP / 16, ND = DP / 32;
+  typedef CLayout<ROWS> L;
+  __shared__ __attribute__((aligned(16))) T sK[L::template size<DP>()];
+  __shared__ __attribute__((aligned(16))) T sV[L::template size<DP>()];
+  __shared__ __attribute__((aligned(16))) float sKn[ROWS];
+
+  if (p.nblk > NB) return;  // the host launches this kernel only for heads that fit
+  const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int N = p.N, D = p.D, org = p.org, nblk = p.nblk;
+  const bool causal = p.causal != 0;
+  const int npre = p.num_prefix;
+  const float c = p.c;
+  const int bh = blockIdx.x;
+  const int b = bh / p.H, hh = bh - b * p.H;
+  const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
+  const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
+  const T* V = reinterpret_cast<const T*>(p.v) + b * p.sv[0] + hh * p.sv[1];
+  const T* Og = reinterpret_cast<const T*>(p.o) + b * p.so[0] + hh * p.so[1];
+  const T* dO = reinterpret_cast<const T*>(p.dout) + b * p.sdo[0] + hh * p.sdo[1];
+  T* dQ = reinterpret_cast<T*>(p.dq) + b * p.sdq[0] + hh * p.sdq[1];
+
+  // Q and dO fragments of one query block, straight to registers.
+  frag qf[KS], df[KS];
+  auto load_qd = [&](int qb) {
+    const int qtok = org + 32 * qb + n;
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      const bool ok = qb >= 0 && qtok >= 0 && 16 * t + 8 * h < D;
+      qf[t] = ok ? ld8<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h) : zero_frag<T>();
+      df[t] = ok ? ld8<T>(dO + (int64_t)qtok * p.sdo[2] + 16 * t + 8 * h) : zero_frag<T>();
+    }
+  };
+  int qb = hr_block(0, wave, W, nblk, causal);
+  load_qd(qb);
+
+  hr_load2<T, ROWS, DP, NT>(K, p.sk[2], sK, V, p.sv[2], sV, 32 * nblk, org, N, D, tid);
+  __syncthreads();
+  hr_neg_halfnorms<T, ROWS, DP, NT>(sK, sKn, 32 * nblk, org, N, tid);
+  __syncthreads();
+
+  const float g2 = 2.f * p.gamma;
+  for (int k = 0; qb >= 0; ++k) {
+    const int q0 = org + 32 * qb, qtok = q0 + n;
+    const bool qvalid = qtok >= 0;
+    const int jmax = last_key(qtok, N, causal, npre);
+    float off, dlt = 0.f;
+    if constexpr (SOFTMAX) {
+      float sdot = 0.f;
+#pragma unroll
+      for (int t = 0; t < KS; ++t) {
+        const bool ok = qvalid && 16 * t + 8 * h < D;
+        const frag of = ok ? ld8<T>(Og + (int64_t)qtok * p.so[2] + 16 * t + 8 * h) : zero_frag<T>();
+        sdot += dot8<T>(of, df[t]);
+      }
+      dlt = xhalf_sum(sdot);
+      off = qvalid ? p.lse[(int64_t)bh * N + qtok] : 0.f;
+      if (qvalid && h == 0) p.delta[(int64_t)bh * N + qtok] = dlt;
+    } else {
+      float ss = 0.f;
+#pragma unroll
+      for (int t = 0; t < KS; ++t) ss += sumsq8<T>(qf[t]);
+      off = c * 0.5f * xhalf_sum(ss);
+      if (qvalid && h == 0) p.lse[(int64_t)bh * N + qtok] = off;
+    }
+    const f32x16_t ndel = splat16(-dlt);
+    // key blocks [0, kend) hold every key some query of the block sees
+    const int kend = causal ? min(nblk, ((max(q0 + 31, npre - 1) - org) >> 5) + 1) : nblk;
+
+    f32x16_t dqacc[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d) dqacc[d] = zero16();
+    float rsum = 0.f;
+    frag kA[KS], vA[KS];
+    auto load_rows = [&](int kb) {
+#pragma unroll
+      for (int t = 0; t < KS; ++t) {
+        kA[t] = ld8<T>(sK + L::off(32 * kb + n, 16 * t + 8 * h));
+        vA[t] = ld8<T>(sV + L::off(32 * kb + n, 16 * t + 8 * h));
+      }
+    };
+    load_rows(0);
+    for (int kb = 0; kb < kend; ++kb) {
+      const int k0 = org + 32 * kb;
+      f32x16_t s = ld_rows16(sKn + 32 * kb, h);
+      f32x16_t dp = ndel;
+#pragma unroll
+      for (int t = 0; t < KS; ++t) {
+        s = E::mma(kA[t], qf[t], s);
+        dp = E::mma(vA[t], df[t], dp);
+      }
+      load_rows(min(kb + 1, kend - 1));
+      // K^T fragments are read while the S / dP MFMAs and the softmax run.
+      frag ktA[ND][2];
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) ktA[d][t] = ld_trc<T, ROWS>(sK, 32 * kb + 16 * t, 32 * d, lane);
+      if (!blk_nomask(q0, k0, causal, npre)) mask_key_rows(s, k0, h, jmax);
+      frag sf[2];
+      float ds[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        ds[i] = fast_exp2(fmaf(s[i], c, -off)) * dp[i];
+        sf[i >> 3][i & 7] = (T)ds[i];
+      }
+      if constexpr (!SOFTMAX) rsum += tree_sum16(ds);
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) dqacc[d] = E::mma(ktA[d][t], sf[t], dqacc[d]);
+    }
+
+    float rs = 0.f;
+    if constexpr (!SOFTMAX) rs = xhalf_sum(rsum);
+    const int qb_next = hr_block(k + 1, wave, W, nblk, causal);
+    if (qvalid) {
+      T* drow = dQ + (int64_t)qtok * p.sdq[2];
+      const T* qrow = Q + (int64_t)qtok * p.sq[2];
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int dd = 32 * d + 8 * g + 4 * h;
+          if (dd < D) {
+            float v4[4];
+            if constexpr (SOFTMAX) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v4[e] = g2 * dqacc[d][4 * g + e];
+            } else {
+              float q4[4];
+              ld4f<T>(qrow + dd, q4);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v4[e] = g2 * (dqacc[d][4 * g + e] - rs * q4[e]);
+            }
+            st4f<T>(drow + dd, v4);
+          }
+        }
+    }
+    qb = qb_next;
+    if (qb >= 0) load_qd(qb);
+  }
+}
+
 }  // namespace rbf

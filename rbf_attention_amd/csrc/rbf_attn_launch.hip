@@ -103,6 +103,13 @@ hipError_t fwd_hr_cfg(const Params& p, hipStream_t st) {
 }
 
 template <int DP, bool SM, int W, int NB>
+hipError_t dq_hr_cfg(const Params& p, hipStream_t st) {
+  hipLaunchKernelGGL((rbf_bwd_dq_hr_kernel<Elt, DP, W, NB, SM>), dim3((unsigned)((long long)p.B * p.H)), dim3(64 * W),
+                     0, st, p);
+  return hipGetLastError();
+}
+
+template <int DP, bool SM, int W, int NB>
 hipError_t dkdv_hr_cfg(const Params& p, hipStream_t st) {
   hipLaunchKernelGGL((rbf_bwd_dkdv_hr_kernel<Elt, DP, W, NB, SM>), dim3((unsigned)((long long)p.B * p.H)),
                      dim3(64 * W), 0, st, p);
@@ -113,9 +120,14 @@ hipError_t dkdv_hr_cfg(const Params& p, hipStream_t st) {
 // tiles (nb_max blocks) and there are at least as many heads as CUs, so one
 // work-group per head fills the GPU.  RBF_ATTN_HR=0 disables them, =1 uses
 // them whenever the head fits.
-bool use_hr(const Params& p, int nb_max) {
+// RBF_ATTN_HR_KERNELS (bits: 1 fwd, 2 dQ, 4 dK/dV) picks which kernels take
+// the head-resident form; the default is fwd and dQ (the head-resident dK/dV
+// measured 46 -> 50 us at C2 on most boxes, against the binned streaming one).
+bool use_hr(const Params& p, int nb_max, int which) {
   static const int forced = env_choice("RBF_ATTN_HR");
-  if (kIsF32 || forced == 0 || p.nblk > nb_max) return false;
+  static const int env_mask = env_choice("RBF_ATTN_HR_KERNELS");
+  const int mask = env_mask >= 0 ? env_mask : 3;
+  if (kIsF32 || forced == 0 || p.nblk > nb_max || !(mask & which)) return false;
   if (forced > 0) return true;
   return (long long)p.B * p.H >= cu_count();
 }
@@ -161,7 +173,7 @@ constexpr int kLongSeq = 2048;
 template <int DP, bool SM>
 hipError_t fwd_default(const Params& p, hipStream_t st) {
   if constexpr (!kIsF32 && DP == 64) {
-    if (use_hr(p, kHrBlocks64)) return fwd_hr_cfg<DP, SM, 12, kHrBlocks64>(p, st);
+    if (use_hr(p, kHrBlocks64, 1)) return fwd_hr_cfg<DP, SM, 12, kHrBlocks64>(p, st);
   }
   if constexpr (kIsF32) return fwd_cfg<DP, SM, 4, 32>(p, st);
   else if constexpr (DP <= 64) {
@@ -174,6 +186,9 @@ hipError_t fwd_default(const Params& p, hipStream_t st) {
 
 template <int DP, bool SM>
 hipError_t dq_default(const Params& p, hipStream_t st) {
+  if constexpr (!kIsF32 && DP == 64) {
+    if (use_hr(p, kHrBlocks64, 2)) return dq_hr_cfg<DP, SM, 8, kHrBlocks64>(p, st);
+  }
   if constexpr (kIsF32) return dq_cfg<DP, SM, 4, 1, 32>(p, st);
   else if constexpr (DP <= 64)
     return bins_fit(p) ? dq_cfg<DP, SM, 4, 1, 128, true, true>(p, st) : dq_cfg<DP, SM, 4, 1, 128>(p, st);
@@ -184,7 +199,7 @@ hipError_t dq_default(const Params& p, hipStream_t st) {
 template <int DP, bool SM>
 hipError_t dkdv_default(const Params& p, hipStream_t st) {
   if constexpr (!kIsF32 && DP == 64) {
-    if (use_hr(p, kHrBlocks64)) return dkdv_hr_cfg<DP, SM, 8, kHrBlocks64>(p, st);
+    if (use_hr(p, kHrBlocks64, 4)) return dkdv_hr_cfg<DP, SM, 8, kHrBlocks64>(p, st);
   }
   if constexpr (kIsF32) return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
   else if constexpr (DP <= 64) {

@@ -225,6 +225,31 @@ def test_queries_far_from_every_key(cuda_device, dtype, shift):
     compare_case(q, k, v, do, gamma=0.0625, tag=f"far{shift} {dtype}")
 
 
+@pytest.mark.parametrize(
+    "N,D,dtype,softmax,causal,num_prefix,shift",
+    [
+        (516, 64, torch.bfloat16, False, True, 0, 0.0),
+        (300, 64, torch.bfloat16, True, False, 0, 0.0),
+        (516, 64, torch.bfloat16, True, True, 4, 0.0),
+        (300, 64, torch.float16, True, True, 0, 0.0),
+        (200, 40, torch.bfloat16, True, True, 0, 0.0),
+        (300, 64, torch.bfloat16, True, True, 0, 6.0),
+    ],
+)
+def test_head_resident_shapes(cuda_device, N, D, dtype, softmax, causal, num_prefix, shift):
+    """B*H = 256 heads of at most 576 tokens: the forward and dQ run as one
+    work-group per head with the head's K and V resident in LDS.  Variants:
+    non-softmax, non-causal, register prefix, fp16 (online max), D = 40, and
+    queries far from every key (the forward's per-block rerun with an online
+    max).  Compared on a 2 x 2 corner of (b, h) slices."""
+    q, k, v, do = rand_inputs(16, 16, N, D, dtype, cuda_device, std=1.0 if softmax else 0.5, seed=N + D)
+    if shift:
+        q = q.clone()
+        q[:2, ::2, :90] += shift
+    compare_case(q, k, v, do, softmax=softmax, causal=causal, num_prefix=num_prefix, gamma=1.0 / (2 * math.sqrt(D)),
+                 sl=(slice(0, 2), slice(0, 2)), tag=f"hr N{N} D{D} {dtype} sm{softmax} c{causal} p{num_prefix} far{shift}")
+
+
 @pytest.mark.parametrize("softmax", [True, False])
 def test_token_major_output(cuda_device, softmax):
     """token_major=True: same values and gradients bit for bit, and the model's
