@@ -120,13 +120,14 @@ hipError_t dkdv_hr_cfg(const Params& p, hipStream_t st) {
 // tiles (nb_max blocks) and there are at least as many heads as CUs, so one
 // work-group per head fills the GPU.  RBF_ATTN_HR=0 disables them, =1 uses
 // them whenever the head fits.
-// RBF_ATTN_HR_KERNELS (bits: 1 fwd, 2 dQ, 4 dK/dV) picks which kernels take
-// the head-resident form; the default is fwd and dQ (the head-resident dK/dV
-// measured 46 -> 50 us at C2 on most boxes, against the binned streaming one).
+// RBF_ATTN_HR_KERNELS (bits: 1 fwd, 2 dQ, 4 dK/dV; default all) picks which
+// kernels take the head-resident form.  The head-resident dK/dV measured
+// faster than the binned streaming one at C2 on four MI355X boxes of five
+// (41-45 against 45-46 us) and slower on one (50 against 46 us).
 bool use_hr(const Params& p, int nb_max, int which) {
   static const int forced = env_choice("RBF_ATTN_HR");
   static const int env_mask = env_choice("RBF_ATTN_HR_KERNELS");
-  const int mask = env_mask >= 0 ? env_mask : 3;
+  const int mask = env_mask >= 0 ? env_mask : 7;
   if (kIsF32 || forced == 0 || p.nblk > nb_max || !(mask & which)) return false;
   if (forced > 0) return true;
   return (long long)p.B * p.H >= cu_count();
