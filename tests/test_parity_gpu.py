@@ -250,6 +250,35 @@ def test_head_resident_shapes(cuda_device, N, D, dtype, softmax, causal, num_pre
                  sl=(slice(0, 2), slice(0, 2)), tag=f"hr N{N} D{D} {dtype} sm{softmax} c{causal} p{num_prefix} far{shift}")
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_flex_attention_cross_check(cuda_device, causal):
+    """Cross-check against torch's own flex_attention on the GPU (the
+    reference's comparator path, rbf_attention.py:1590-1605, run in fp32 on
+    the same bf16 inputs, unfused): O and the autograd gradients agree with
+    the HIP kernels to the bf16 tolerance, and flex itself agrees with the
+    float64 oracle."""
+    import warnings
+
+    from rbf_attention_amd.flex import rbf_flex_attention
+
+    w = wl.C2_MODEL.with_(B=2, H=4)
+    q, k, v, do = to_dev(wl.make_inputs(w), cuda_device)
+    g = w.sm_scale
+    ours = run_ours(q, k, v, do, True, causal, g, 0)
+    qf, kf, vf = (t.detach().float().clone().requires_grad_(True) for t in (q, k, v))
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        of = rbf_flex_attention(qf, kf, vf, is_causal=causal, sm_scale=g)
+    of.backward(do.float())
+    torch.cuda.synchronize()
+    flex = (of, qf.grad, kf.grad, vf.grad)
+    refs, _ = oracle_all(q, k, v, do, True, causal, g, 0)
+    for name, a, f, r in zip(("O", "dQ", "dK", "dV"), ours, flex, refs):
+        check(f"flex c{causal} {name} (ours vs flex)", a, np64(f), q.dtype)
+        fe = float(np.abs(np64(f) - r).max())
+        assert fe <= 1e-3 * max(1.0, float(np.abs(r).max())), f"flex vs oracle {name}: {fe}"
+
+
 @pytest.mark.parametrize("softmax", [True, False])
 def test_token_major_output(cuda_device, softmax):
     """token_major=True: same values and gradients bit for bit, and the model's
