@@ -56,6 +56,7 @@ extern "C" {
 #define RBF_ATTN_EINVAL_SHAPE -5   /* negative sizes, grid too large        */
 #define RBF_ATTN_EINVAL_PTR -6     /* a required pointer is NULL            */
 #define RBF_ATTN_ELAUNCH -7        /* the HIP runtime rejected a launch     */
+#define RBF_ATTN_EUNSUPPORTED -8   /* valid, but outside a fused path's set */
 
 /* One (B, H, N, D) operand: base pointer and element strides of dims 0-2. */
 typedef struct rbf_attn_tensor {
@@ -119,6 +120,27 @@ int rbf_attn_bwd(const rbf_attn_args* args, void* stream);
  * any other stage value returns RBF_ATTN_EINVAL_ARGS.
  */
 int rbf_attn_bwd_stage(const rbf_attn_args* args, void* stream, int stage);
+
+/*
+ * Forward / backward with a position term fused into the Q and K reads:
+ * the kernels use q + pos and k + pos (each sum rounded to the element type,
+ * as two separate elementwise adds of the tensors would store it) wherever
+ * the plain entry points use q and k.  pos is a (B, H, N, D) operand like
+ * the others (stride_b may be 0: one term shared by the batch).  The
+ * gradients dq, dk are those of the shifted inputs, which equal the
+ * gradients of q, k; the term's own gradient is sum_b (dq + dk) and is left
+ * to the caller.  No reference counterpart: it fuses the SuSiE position
+ * embedding of the reference model (rbf_attention.py:1666-1688,
+ * `q, k = q + pos_emb, k + pos_emb`) into the attention kernels.  Supported
+ * for bf16/fp16, 32 < D <= 64, N <= 576 (the head-resident kernels);
+ * otherwise RBF_ATTN_EUNSUPPORTED before any launch.
+ */
+int rbf_attn_fwd_pos(const rbf_attn_args* args, const rbf_attn_tensor* pos, void* stream);
+int rbf_attn_bwd_pos(const rbf_attn_args* args, const rbf_attn_tensor* pos, void* stream);
+
+/* 1 if rbf_attn_fwd_pos / rbf_attn_bwd_pos support args (shape, dtype), 0 if
+ * not, or a negative error code for invalid args.  No reference counterpart. */
+int rbf_attn_pos_supported(const rbf_attn_args* args);
 
 /*
  * Decode against a KV cache: T new query tokens per (batch, head) attend to

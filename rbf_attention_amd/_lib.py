@@ -30,6 +30,7 @@ ERRORS = {
     -5: "EINVAL_SHAPE",
     -6: "EINVAL_PTR",
     -7: "ELAUNCH",
+    -8: "EUNSUPPORTED",
 }
 
 # Every extern "C" entry point of include/rbf_attn.h.
@@ -37,6 +38,9 @@ EXPORTS = (
     "rbf_attn_fwd",
     "rbf_attn_bwd",
     "rbf_attn_bwd_stage",
+    "rbf_attn_fwd_pos",
+    "rbf_attn_bwd_pos",
+    "rbf_attn_pos_supported",
     "rbf_attn_decode_workspace_size",
     "rbf_attn_decode",
     "rbf_attn_last_error",
@@ -146,6 +150,12 @@ def load(path: str | None = None):
         lib.rbf_attn_bwd.restype = ctypes.c_int
         lib.rbf_attn_bwd_stage.argtypes = [ctypes.POINTER(Args), ctypes.c_void_p, ctypes.c_int]
         lib.rbf_attn_bwd_stage.restype = ctypes.c_int
+        lib.rbf_attn_fwd_pos.argtypes = [ctypes.POINTER(Args), ctypes.POINTER(Tensor), ctypes.c_void_p]
+        lib.rbf_attn_fwd_pos.restype = ctypes.c_int
+        lib.rbf_attn_bwd_pos.argtypes = [ctypes.POINTER(Args), ctypes.POINTER(Tensor), ctypes.c_void_p]
+        lib.rbf_attn_bwd_pos.restype = ctypes.c_int
+        lib.rbf_attn_pos_supported.argtypes = [ctypes.POINTER(Args)]
+        lib.rbf_attn_pos_supported.restype = ctypes.c_int
         lib.rbf_attn_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs)]
         lib.rbf_attn_decode_workspace_size.restype = ctypes.c_uint64
         lib.rbf_attn_decode.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]
@@ -185,3 +195,18 @@ def call(fn_name: str, args, stream: int, *extra: int) -> None:
     if rc != 0:
         msg = lib.rbf_attn_last_error().decode(errors="replace")
         raise RbfAttnError(rc, msg)
+
+
+def pos_supported(args: Args) -> bool:
+    """Whether rbf_attn_{fwd,bwd}_pos fuse a position term for these args."""
+    rc = load().rbf_attn_pos_supported(ctypes.byref(args))
+    if rc < 0:
+        raise RbfAttnError(rc, load().rbf_attn_last_error().decode(errors="replace"))
+    return rc == 1
+
+
+def call_pos(fn_name: str, args, pos: Tensor, stream: int) -> None:
+    lib = load()
+    rc = getattr(lib, fn_name)(ctypes.byref(args), ctypes.byref(pos), ctypes.c_void_p(stream))
+    if rc != 0:
+        raise RbfAttnError(rc, lib.rbf_attn_last_error().decode(errors="replace"))

@@ -242,7 +242,26 @@ int rbf_attn_abi_version(void) { return RBF_ATTN_ABI_VERSION; }
 
 const char* rbf_attn_last_error(void) { return g_err; }
 
-int rbf_attn_fwd(const rbf_attn_args* a, void* stream) {
+// Checks a position term for rbf_attn_{fwd,bwd}_pos and stores it in p.
+static int set_pos(const rbf_attn_args* a, const rbf_attn_tensor* pos, rbf::Params& p) {
+  int rc;
+  if (pos == nullptr) return fail(RBF_ATTN_EINVAL_PTR, "pos: null descriptor");
+  if ((rc = check_tensor("pos", *pos, elem_size(a->dtype)))) return rc;
+  if (rbf_attn_pos_supported(a) != 1)
+    return fail(RBF_ATTN_EUNSUPPORTED, "position term fused only for bf16/fp16, 32 < D <= 64, N <= 576 (D=%d N=%d)", a->D,
+                a->N);
+  p.pos = pos->ptr;
+  copy_strides(p.spos, *pos);
+  return RBF_ATTN_OK;
+}
+
+int rbf_attn_pos_supported(const rbf_attn_args* a) {
+  int rc = check_common(a);
+  if (rc) return rc;
+  return (a->dtype != RBF_ATTN_FP32 && a->D > 32 && a->D <= 64 && a->N <= 576) ? 1 : 0;
+}
+
+static int fwd_impl(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* stream) {
   int rc = check_common(a);
   if (rc) return rc;
   const size_t esz = elem_size(a->dtype);
@@ -252,7 +271,8 @@ int rbf_attn_fwd(const rbf_attn_args* a, void* stream) {
   if ((rc = check_tensor("o", a->o, esz))) return rc;
   if (a->variant == RBF_ATTN_SOFTMAX && (rc = check_f32("lse", a->lse))) return rc;
   if ((long long)a->B * a->H * a->N == 0) return RBF_ATTN_OK;
-  const rbf::Params p = make_params(a);
+  rbf::Params p = make_params(a);
+  if (pos && (rc = set_pos(a, pos, p))) return rc;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   switch (a->dtype) {
@@ -263,7 +283,16 @@ int rbf_attn_fwd(const rbf_attn_args* a, void* stream) {
   return launched(e, "forward");
 }
 
-static int bwd_impl(const rbf_attn_args* a, void* stream, int stage) {
+int rbf_attn_fwd(const rbf_attn_args* a, void* stream) { return fwd_impl(a, nullptr, stream); }
+int rbf_attn_fwd_pos(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* stream) {
+  if (pos == nullptr) {
+    g_err[0] = '\0';
+    return fail(RBF_ATTN_EINVAL_PTR, "pos: null descriptor");
+  }
+  return fwd_impl(a, pos, stream);
+}
+
+static int bwd_impl(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* stream, int stage) {
   int rc = check_common(a);
   if (rc) return rc;
   if (stage < 0 || stage > 2) return fail(RBF_ATTN_EINVAL_ARGS, "unknown backward stage %d", stage);
@@ -281,7 +310,8 @@ static int bwd_impl(const rbf_attn_args* a, void* stream, int stage) {
     if ((rc = check_f32("delta", a->delta))) return rc;
   }
   if ((long long)a->B * a->H * a->N == 0) return RBF_ATTN_OK;
-  const rbf::Params p = make_params(a);
+  rbf::Params p = make_params(a);
+  if (pos && (rc = set_pos(a, pos, p))) return rc;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   if (stage == 0 || stage == 1) {
@@ -303,14 +333,22 @@ static int bwd_impl(const rbf_attn_args* a, void* stream, int stage) {
   return RBF_ATTN_OK;
 }
 
-int rbf_attn_bwd(const rbf_attn_args* a, void* stream) { return bwd_impl(a, stream, 0); }
+int rbf_attn_bwd(const rbf_attn_args* a, void* stream) { return bwd_impl(a, nullptr, stream, 0); }
+
+int rbf_attn_bwd_pos(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* stream) {
+  if (pos == nullptr) {
+    g_err[0] = '\0';
+    return fail(RBF_ATTN_EINVAL_PTR, "pos: null descriptor");
+  }
+  return bwd_impl(a, pos, stream, 0);
+}
 
 int rbf_attn_bwd_stage(const rbf_attn_args* a, void* stream, int stage) {
   if (stage != 1 && stage != 2) {
     g_err[0] = '\0';
     return fail(RBF_ATTN_EINVAL_ARGS, "unknown backward stage %d", stage);
   }
-  return bwd_impl(a, stream, stage);
+  return bwd_impl(a, nullptr, stream, stage);
 }
 
 }  // extern "C"

@@ -11,6 +11,12 @@
 // Waves take their blocks in snake order over the causal weights (heaviest
 // first), so each wave -- and each SIMD -- gets a near-equal share of the
 // head's 32x32 block pairs.
+//
+// POS: a position term P (Params::pos) is added to Q and K as they are read
+// (q + P and k + P, each sum rounded to the element type, as the separate
+// elementwise adds of the model would store them): the SuSiE position
+// embedding of the reference model (rbf_attention.py:1666-1688) fused into
+// the loads.
 #pragma once
 
 #include "rbf_attn_kernels.h"
@@ -29,13 +35,15 @@ __device__ inline void hr_unit(int u, int& row, int& ch) {
 
 // Loads rows [0, rows) -- tokens org + row -- of two (N, D) slices into
 // chunk-major LDS tiles of ROWS rows; tokens outside [0, N) and features
-// >= D are zero.  Every chunk of a thread is requested before the first is
+// >= D are zero; addA (row stride asa), when not null, is added to every row
+// of the first slice (position term).  Every chunk of a thread is requested
+// before the first is
 // stored.  The code is branch-free: with conditional stores here the compiler's
 // wait-count insertion no longer tells later LDS reads of other tiles apart
 // from outstanding LDS-DMA loads, and makes them wait for those loads.
 template <typename T, int ROWS, int DP, int NT>
 __device__ inline void hr_load2(const T* A, int64_t sa, T* sA, const T* B, int64_t sb, T* sB, int rows, int org,
-                                int N, int D, int tid) {
+                                int N, int D, int tid, const T* addA = nullptr, int64_t asa = 0) {
   typedef typename Elem<T>::frag frag;
   typedef CLayout<ROWS> L;
   constexpr int PB = (ROWS * (DP / 8) + NT - 1) / NT;
@@ -48,7 +56,8 @@ __device__ inline void hr_load2(const T* A, int64_t sa, T* sA, const T* B, int64
     hr_unit<DP>(u, row, ch);
     const int tok = org + row;
     const bool ok = u < units && tok >= 0 && tok < N && ch * 8 < D;
-    ra[j] = ok ? ld8<T>(A + (int64_t)tok * sa + ch * 8) : zero_frag<T>();
+    ra[j] = ok ? ld8p<T>(A + (int64_t)tok * sa + ch * 8, addA ? addA + (int64_t)tok * asa + ch * 8 : nullptr)
+               : zero_frag<T>();
     rb[j] = ok ? ld8<T>(B + (int64_t)tok * sb + ch * 8) : zero_frag<T>();
   }
   // Units past the tile store into the padding after chunk column 0 instead
@@ -101,7 +110,7 @@ __device__ inline int hr_block(int k, int wave, int W, int nblk, bool reverse) {
 // MFMA and VALU work of one wave overlap.  Only the causal diagonal block
 // needs a mask; it is peeled off the loop.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int NB, bool SOFTMAX>
+template <typename T, int DP, int W, int NB, bool SOFTMAX, bool POS = false>
 __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -123,6 +132,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
   const int b = bh / p.H, hh = bh - b * p.H;
   const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
   const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
+  const T* Pos = POS ? reinterpret_cast<const T*>(p.pos) + b * p.spos[0] + hh * p.spos[1] : nullptr;
   const T* V = reinterpret_cast<const T*>(p.v) + b * p.sv[0] + hh * p.sv[1];
   T* O = reinterpret_cast<T*>(const_cast<void*>(p.o)) + b * p.so[0] + hh * p.so[1];
 
@@ -130,15 +140,17 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
     const int qtok = org + 32 * qb + n;
 #pragma unroll
     for (int t = 0; t < KS; ++t)
-      qf[t] = (qb >= 0 && qtok >= 0 && 16 * t + 8 * h < D) ? ld8<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h)
-                                                            : zero_frag<T>();
+      qf[t] = (qb >= 0 && qtok >= 0 && 16 * t + 8 * h < D)
+                  ? ld8p<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h,
+                            Pos ? Pos + (int64_t)qtok * p.spos[2] + 16 * t + 8 * h : nullptr)
+                  : zero_frag<T>();
   };
   // The first query block's Q fragments are requested before the K/V load.
   frag qf[KS];
   int qb = hr_block(0, wave, W, nblk, causal);
   load_q(qb, qf);
 
-  hr_load2<T, ROWS, DP, NT>(K, p.sk[2], sK, V, p.sv[2], sV, 32 * nblk, org, N, D, tid);
+  hr_load2<T, ROWS, DP, NT>(K, p.sk[2], sK, V, p.sv[2], sV, 32 * nblk, org, N, D, tid, Pos, p.spos[2]);
   __syncthreads();
   hr_neg_halfnorms<T, ROWS, DP, NT>(sK, sKn, 32 * nblk, org, N, tid);
   __syncthreads();
@@ -308,7 +320,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
 //   -Delta), dS = P dP, dV^T += dO^T P, dK^T += Q^T dS, colsum += dS,
 // with K and V in registers and no barrier after the load.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int NB, bool SOFTMAX>
+template <typename T, int DP, int W, int NB, bool SOFTMAX, bool POS = false>
 __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -332,6 +344,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
   const int b = bh / p.H, hh = bh - b * p.H;
   const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
   const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
+  const T* Pos = POS ? reinterpret_cast<const T*>(p.pos) + b * p.spos[0] + hh * p.spos[1] : nullptr;
   const T* V = reinterpret_cast<const T*>(p.v) + b * p.sv[0] + hh * p.sv[1];
   const T* dO = reinterpret_cast<const T*>(p.dout) + b * p.sdo[0] + hh * p.sdo[1];
   T* dK = reinterpret_cast<T*>(p.dk) + b * p.sdk[0] + hh * p.sdk[1];
@@ -348,7 +361,9 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
       const bool ok = kb >= 0 && ktok >= 0 && 16 * t + 8 * h < D;
-      kf[t] = ok ? ld8<T>(K + (int64_t)ktok * p.sk[2] + 16 * t + 8 * h) : zero_frag<T>();
+      kf[t] = ok ? ld8p<T>(K + (int64_t)ktok * p.sk[2] + 16 * t + 8 * h,
+                           Pos ? Pos + (int64_t)ktok * p.spos[2] + 16 * t + 8 * h : nullptr)
+                 : zero_frag<T>();
       vf[t] = ok ? ld8<T>(V + (int64_t)ktok * p.sv[2] + 16 * t + 8 * h) : zero_frag<T>();
       ss += sumsq8<T>(kf[t]);
     }
@@ -357,7 +372,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
   int kb = hr_block(0, wave, W, nblk, false);
   load_kv(kb);
 
-  hr_load2<T, ROWS, DP, NT>(Q, p.sq[2], sQ, dO, p.sdo[2], sD, 32 * nblk, org, N, D, tid);
+  hr_load2<T, ROWS, DP, NT>(Q, p.sq[2], sQ, dO, p.sdo[2], sD, 32 * nblk, org, N, D, tid, Pos, p.spos[2]);
   for (int r = tid; r < 32 * nblk; r += NT) {
     const int tok = org + r;
     const bool ok = tok >= 0 && tok < N;
@@ -444,7 +459,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
           const int dd = 32 * d + 8 * g + 4 * h;
           if (dd < D) {
             float k4[4], a4[4], b4[4];
-            ld4f<T>(krow + dd, k4);
+            ld4fp<T>(krow + dd, Pos ? Pos + (int64_t)ktok * p.spos[2] + dd : nullptr, k4);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               a4[e] = g2 * (dkacc[d][4 * g + e] - cs * k4[e]);
@@ -471,7 +486,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
 // with the next key block's K and V rows read one block ahead and no
 // barrier after the load.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int NB, bool SOFTMAX>
+template <typename T, int DP, int W, int NB, bool SOFTMAX, bool POS = false>
 __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -493,6 +508,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
   const int b = bh / p.H, hh = bh - b * p.H;
   const T* Q = reinterpret_cast<const T*>(p.q) + b * p.sq[0] + hh * p.sq[1];
   const T* K = reinterpret_cast<const T*>(p.k) + b * p.sk[0] + hh * p.sk[1];
+  const T* Pos = POS ? reinterpret_cast<const T*>(p.pos) + b * p.spos[0] + hh * p.spos[1] : nullptr;
   const T* V = reinterpret_cast<const T*>(p.v) + b * p.sv[0] + hh * p.sv[1];
   const T* Og = reinterpret_cast<const T*>(p.o) + b * p.so[0] + hh * p.so[1];
   const T* dO = reinterpret_cast<const T*>(p.dout) + b * p.sdo[0] + hh * p.sdo[1];
@@ -505,14 +521,16 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
       const bool ok = qb >= 0 && qtok >= 0 && 16 * t + 8 * h < D;
-      qf[t] = ok ? ld8<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h) : zero_frag<T>();
+      qf[t] = ok ? ld8p<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h,
+                           Pos ? Pos + (int64_t)qtok * p.spos[2] + 16 * t + 8 * h : nullptr)
+                 : zero_frag<T>();
       df[t] = ok ? ld8<T>(dO + (int64_t)qtok * p.sdo[2] + 16 * t + 8 * h) : zero_frag<T>();
     }
   };
   int qb = hr_block(0, wave, W, nblk, causal);
   load_qd(qb);
 
-  hr_load2<T, ROWS, DP, NT>(K, p.sk[2], sK, V, p.sv[2], sV, 32 * nblk, org, N, D, tid);
+  hr_load2<T, ROWS, DP, NT>(K, p.sk[2], sK, V, p.sv[2], sV, 32 * nblk, org, N, D, tid, Pos, p.spos[2]);
   __syncthreads();
   hr_neg_halfnorms<T, ROWS, DP, NT>(sK, sKn, 32 * nblk, org, N, tid);
   __syncthreads();
@@ -607,7 +625,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
               for (int e = 0; e < 4; ++e) v4[e] = g2 * dqacc[d][4 * g + e];
             } else {
               float q4[4];
-              ld4f<T>(qrow + dd, q4);
+              ld4fp<T>(qrow + dd, Pos ? Pos + (int64_t)qtok * p.spos[2] + dd : nullptr, q4);
 #pragma unroll
               for (int e = 0; e < 4; ++e) v4[e] = g2 * (dqacc[d][4 * g + e] - rs * q4[e]);
             }

@@ -73,6 +73,9 @@ struct Params {
   int nblk;          // number of 32-token blocks
   int hchunk;        // heads per heaviest-first chunk on one XCD (>= 1)
   int nbin;          // work-groups per head (set per launch; each runs a bin of groups)
+  const void* pos;   // position term added to Q and K as they are read (null: none;
+                     // only the head-resident kernels read it)
+  int64_t spos[3];   // its (b, h, n) strides; b may be 0 (shared by the batch)
 };
 
 // ---------------------------------------------------------------------------
@@ -138,6 +141,24 @@ __device__ inline void st8(T* p, typename Elem<T>::frag f) {
   *reinterpret_cast<raw16*>(p) = __builtin_bit_cast(raw, f);
 }
 
+// a + b in fp32, rounded to the element type: what an elementwise add of two
+// element-type tensors stores.
+template <typename T>
+__device__ inline typename Elem<T>::frag add8(typename Elem<T>::frag a, typename Elem<T>::frag b) {
+  typename Elem<T>::frag r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (T)((float)a[e] + (float)b[e]);
+  return r;
+}
+
+// 8 elements at p, plus the 8 at pp when pp is not null (the position term
+// of a Q or K row).
+template <typename T>
+__device__ inline typename Elem<T>::frag ld8p(const T* p, const T* pp) {
+  const typename Elem<T>::frag x = ld8<T>(p);
+  return pp ? add8<T>(x, ld8<T>(pp)) : x;
+}
+
 // 4 consecutive elements (8-byte aligned for 16-bit types, 16 for fp32).
 template <typename T>
 __device__ inline void ld4f(const T* p, float out[4]) {
@@ -146,6 +167,18 @@ __device__ inline void ld4f(const T* p, float out[4]) {
   quad v = *reinterpret_cast<const quadA*>(p);
 #pragma unroll
   for (int e = 0; e < 4; ++e) out[e] = (float)v[e];
+}
+
+// ld4f of p, plus pp (rounded to the element type, as add8) when not null.
+template <typename T>
+__device__ inline void ld4fp(const T* p, const T* pp, float out[4]) {
+  ld4f<T>(p, out);
+  if (pp) {
+    float a[4];
+    ld4f<T>(pp, a);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = (float)(T)(out[e] + a[e]);
+  }
 }
 
 template <typename T>

@@ -95,23 +95,23 @@ hipError_t launch(F kernel, const Params& p, int blocks_per_wg, int threads, int
   return hipGetLastError();
 }
 
-template <int DP, bool SM, int W, int NB>
+template <int DP, bool SM, int W, int NB, bool POS = false>
 hipError_t fwd_hr_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_fwd_hr_kernel<Elt, DP, W, NB, SM>), dim3((unsigned)((long long)p.B * p.H)), dim3(64 * W), 0,
+  hipLaunchKernelGGL((rbf_fwd_hr_kernel<Elt, DP, W, NB, SM, POS>), dim3((unsigned)((long long)p.B * p.H)), dim3(64 * W), 0,
                      st, p);
   return hipGetLastError();
 }
 
-template <int DP, bool SM, int W, int NB>
+template <int DP, bool SM, int W, int NB, bool POS = false>
 hipError_t dq_hr_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_bwd_dq_hr_kernel<Elt, DP, W, NB, SM>), dim3((unsigned)((long long)p.B * p.H)), dim3(64 * W),
+  hipLaunchKernelGGL((rbf_bwd_dq_hr_kernel<Elt, DP, W, NB, SM, POS>), dim3((unsigned)((long long)p.B * p.H)), dim3(64 * W),
                      0, st, p);
   return hipGetLastError();
 }
 
-template <int DP, bool SM, int W, int NB>
+template <int DP, bool SM, int W, int NB, bool POS = false>
 hipError_t dkdv_hr_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_bwd_dkdv_hr_kernel<Elt, DP, W, NB, SM>), dim3((unsigned)((long long)p.B * p.H)),
+  hipLaunchKernelGGL((rbf_bwd_dkdv_hr_kernel<Elt, DP, W, NB, SM, POS>), dim3((unsigned)((long long)p.B * p.H)),
                      dim3(64 * W), 0, st, p);
   return hipGetLastError();
 }
@@ -171,8 +171,16 @@ hipError_t dkdv_pair_cfg(const Params& p, hipStream_t st) {
 // head has enough tokens to keep them busy.
 constexpr int kLongSeq = 2048;
 
+// With a position term (Params::pos) only the head-resident kernels apply;
+// the C ABI admits it for 16-bit elements, 32 < D <= 64 and N <= 576.
 template <int DP, bool SM>
 hipError_t fwd_default(const Params& p, hipStream_t st) {
+  if (p.pos) {
+    if constexpr (!kIsF32 && DP == 64) {
+      if (p.nblk <= kHrBlocks64) return fwd_hr_cfg<DP, SM, 12, kHrBlocks64, true>(p, st);
+    }
+    return hipErrorInvalidValue;
+  }
   if constexpr (!kIsF32 && DP == 64) {
     if (use_hr(p, kHrBlocks64, 1)) return fwd_hr_cfg<DP, SM, 12, kHrBlocks64>(p, st);
   }
@@ -187,6 +195,12 @@ hipError_t fwd_default(const Params& p, hipStream_t st) {
 
 template <int DP, bool SM>
 hipError_t dq_default(const Params& p, hipStream_t st) {
+  if (p.pos) {
+    if constexpr (!kIsF32 && DP == 64) {
+      if (p.nblk <= kHrBlocks64) return dq_hr_cfg<DP, SM, 8, kHrBlocks64, true>(p, st);
+    }
+    return hipErrorInvalidValue;
+  }
   if constexpr (!kIsF32 && DP == 64) {
     if (use_hr(p, kHrBlocks64, 2)) return dq_hr_cfg<DP, SM, 8, kHrBlocks64>(p, st);
   }
@@ -199,6 +213,12 @@ hipError_t dq_default(const Params& p, hipStream_t st) {
 
 template <int DP, bool SM>
 hipError_t dkdv_default(const Params& p, hipStream_t st) {
+  if (p.pos) {
+    if constexpr (!kIsF32 && DP == 64) {
+      if (p.nblk <= kHrBlocks64) return dkdv_hr_cfg<DP, SM, 8, kHrBlocks64, true>(p, st);
+    }
+    return hipErrorInvalidValue;
+  }
   if constexpr (!kIsF32 && DP == 64) {
     if (use_hr(p, kHrBlocks64, 4)) return dkdv_hr_cfg<DP, SM, 8, kHrBlocks64>(p, st);
   }
@@ -218,6 +238,7 @@ hipError_t dkdv_default(const Params& p, hipStream_t st) {
 // ---- tuning candidates (bf16, 32 < D <= 64) ------------------------------
 template <int DP, bool SM>
 hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
+  if (p.pos) return fwd_default<DP, SM>(p, st);  // tuning candidates take no position term
 #if RBF_ELEM_ID == 0
   static const int choice = env_choice("RBF_ATTN_FWD_CFG");
   switch (choice) {
@@ -241,6 +262,7 @@ hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
 
 template <int DP, bool SM>
 hipError_t dq_any_cfg(const Params& p, hipStream_t st) {
+  if (p.pos) return dq_default<DP, SM>(p, st);  // tuning candidates take no position term
 #if RBF_ELEM_ID == 0
   if constexpr (DP == 128) {
     static const int choice = env_choice("RBF_ATTN_DQ_CFG");
@@ -273,6 +295,7 @@ hipError_t dq_any_cfg(const Params& p, hipStream_t st) {
 
 template <int DP, bool SM>
 hipError_t dkdv_any_cfg(const Params& p, hipStream_t st) {
+  if (p.pos) return dkdv_default<DP, SM>(p, st);  // tuning candidates take no position term
 #if RBF_ELEM_ID == 0
   if constexpr (DP == 128) {
     static const int choice = env_choice("RBF_ATTN_DKDV_CFG");

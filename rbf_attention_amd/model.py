@@ -88,12 +88,14 @@ class RBFAttention(nn.Module):
         qkv = self.qkv_proj(x)
         # "b s (qkv h n) -> qkv b h s n" as strided views (rbf_attention.py:1660-1662)
         q, k, v = qkv.view(b, s, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4)
-        if self.use_susie:
-            pos = self.position_embedding(s, q.dtype)
-            q, k = q + pos, k + pos
+        # SuSiE: attention of q + pos and k + pos (rbf_attention.py:1666-1688),
+        # with the add fused into the kernels' Q/K reads where the library
+        # supports the shape
+        pos = self.position_embedding(s, q.dtype) if self.use_susie else None
         fn = ops.run_triton_rbf if self.attention_type == "rbf" else ops.run_triton_non_softmax_rbf
         # token-major output: the transpose + reshape below is then a view
-        out = fn(q, k, v, True, sm_scale=self.sm_scale, num_prefix=self.num_prefix, token_major=not self.apply_xsa)
+        out = fn(q, k, v, True, sm_scale=self.sm_scale, num_prefix=self.num_prefix, token_major=not self.apply_xsa,
+                 pos=pos)
         if self.apply_xsa:
             v_n = F.normalize(v, dim=-1)
             out = out - (out * v_n).sum(dim=-1, keepdim=True) * v_n

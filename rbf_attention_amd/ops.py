@@ -28,6 +28,7 @@ fallback.  Unsupported inputs raise.
 from __future__ import annotations
 
 import math
+from typing import Optional
 
 import torch
 
@@ -101,6 +102,35 @@ def _launch(fn: str, a, device: torch.device) -> None:
         _lib.call(fn, a, torch.cuda.current_stream(device).cuda_stream)
 
 
+def _launch_pos(fn: str, a, pos: torch.Tensor, device: torch.device) -> None:
+    if a.B * a.H * a.N == 0:
+        return
+    with torch.cuda.device(device):
+        _lib.call_pos(fn, a, _lib.tensor_desc(pos), torch.cuda.current_stream(device).cuda_stream)
+
+
+def _check_pos(name: str, q: torch.Tensor, pos: torch.Tensor) -> None:
+    B, H, N, D = q.shape
+    if pos.dim() != 4 or tuple(pos.shape[1:]) != (H, N, D) or pos.shape[0] not in (1, B):
+        raise ValueError(f"{name}: pos must be (1 or B, H, N, D) = (1|{B}, {H}, {N}, {D}), got {tuple(pos.shape)}")
+    if pos.dtype != q.dtype or pos.device != q.device:
+        raise TypeError(f"{name}: pos must match q's dtype and device")
+
+
+def _with_pos(name: str, a, q, k, pos, dp: int):
+    """Position term for a launch: the (B, H, N, dp) operand for the fused
+    entry points when the library fuses it for these args (the head-resident
+    kernels), else None after adding it to q and k here -- the same values
+    (each sum rounded to the element type), as separate elementwise adds."""
+    if pos is None:
+        return q, k, None
+    _check_pos(name, q, pos)
+    if _lib.pos_supported(a):
+        B, H, N, _ = q.shape
+        return q, k, _prep(pos, dp).expand(B, H, N, dp)
+    return q + pos, k + pos, None
+
+
 def _unpad(t: torch.Tensor, d: int) -> torch.Tensor:
     return t if t.shape[-1] == d else t[..., :d].contiguous()
 
@@ -118,67 +148,84 @@ def _alloc_out(q: torch.Tensor, dp: int, token_major: bool) -> torch.Tensor:
     return torch.empty((B, H, N, dp), device=q.device, dtype=q.dtype)
 
 
-def _softmax_fwd(q, k, v, is_causal: bool, sm_scale: float, num_prefix: int, token_major: bool = False):
+def _softmax_fwd(q, k, v, is_causal: bool, sm_scale: float, num_prefix: int, token_major: bool = False, pos=None):
     _check_inputs("scaled_fwd", q, k, v)
     B, H, N, D = q.shape
     dp = _padded_dim(D)
+    a = _base_args(_lib.SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
+    q, k, pos_ = _with_pos("scaled_fwd", a, q, k, pos, dp)
     q_, k_, v_ = _prep(q, dp), _prep(k, dp), _prep(v, dp)
     out = _alloc_out(q, dp, token_major and dp == D)
     L = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
-    a = _base_args(_lib.SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
     a.q, a.k, a.v, a.o = (_lib.tensor_desc(t) for t in (q_, k_, v_, out))
     a.lse = L.data_ptr()
-    _launch("rbf_attn_fwd", a, q.device)
+    if pos_ is None:
+        _launch("rbf_attn_fwd", a, q.device)
+    else:
+        _launch_pos("rbf_attn_fwd_pos", a, pos_, q.device)
     return _unpad(out, D), L
 
 
-def _softmax_bwd(q, k, v, out, L, dout, is_causal: bool, sm_scale: float, num_prefix: int):
+def _softmax_bwd(q, k, v, out, L, dout, is_causal: bool, sm_scale: float, num_prefix: int, pos=None):
     _check_inputs("scaled_bwd", q, k, v, out, dout)
     B, H, N, D = q.shape
     if L.shape != (B, H, N) or L.dtype != torch.float32:
         raise ValueError(f"scaled_bwd: L must be float32 of shape {(B, H, N)}, got {L.dtype} {tuple(L.shape)}")
     dp = _padded_dim(D)
+    a = _base_args(_lib.SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
+    q, k, pos_ = _with_pos("scaled_bwd", a, q, k, pos, dp)
     q_, k_, v_, o_, do_ = (_prep(t, dp) for t in (q, k, v, out, dout))
     L_ = L.contiguous()
     delta = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
     dq = torch.empty((B, H, N, dp), device=q.device, dtype=q.dtype)
     dk = torch.empty_like(dq)
     dv = torch.empty_like(dq)
-    a = _base_args(_lib.SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
     a.q, a.k, a.v, a.o, a.dout = (_lib.tensor_desc(t) for t in (q_, k_, v_, o_, do_))
     a.dq, a.dk, a.dv = (_lib.tensor_desc(t) for t in (dq, dk, dv))
     a.lse = L_.data_ptr()
     a.delta = delta.data_ptr()
-    _launch("rbf_attn_bwd", a, q.device)
+    if pos_ is None:
+        _launch("rbf_attn_bwd", a, q.device)
+    else:
+        _launch_pos("rbf_attn_bwd_pos", a, pos_, q.device)
     return _unpad(dq, D), _unpad(dk, D), _unpad(dv, D)
 
 
-def _non_softmax_fwd(q, k, v, is_causal: bool, sm_scale: float, num_prefix: int, token_major: bool = False):
+def _non_softmax_fwd(q, k, v, is_causal: bool, sm_scale: float, num_prefix: int, token_major: bool = False,
+                     pos=None):
     _check_inputs("non_softmax_fwd", q, k, v)
     B, H, N, D = q.shape
     dp = _padded_dim(D)
+    a = _base_args(_lib.NON_SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
+    q, k, pos_ = _with_pos("non_softmax_fwd", a, q, k, pos, dp)
     q_, k_, v_ = _prep(q, dp), _prep(k, dp), _prep(v, dp)
     out = _alloc_out(q, dp, token_major and dp == D)
-    a = _base_args(_lib.NON_SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
     a.q, a.k, a.v, a.o = (_lib.tensor_desc(t) for t in (q_, k_, v_, out))
-    _launch("rbf_attn_fwd", a, q.device)
+    if pos_ is None:
+        _launch("rbf_attn_fwd", a, q.device)
+    else:
+        _launch_pos("rbf_attn_fwd_pos", a, pos_, q.device)
     return _unpad(out, D)
 
 
-def _non_softmax_bwd(q, k, v, dout, is_causal: bool, sm_scale: float, num_prefix: int):
+def _non_softmax_bwd(q, k, v, dout, is_causal: bool, sm_scale: float, num_prefix: int, pos=None):
     _check_inputs("non_softmax_bwd", q, k, v, dout)
     B, H, N, D = q.shape
     dp = _padded_dim(D)
+    a = _base_args(_lib.NON_SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
+    q, k, pos_ = _with_pos("non_softmax_bwd", a, q, k, pos, dp)
     q_, k_, v_, do_ = (_prep(t, dp) for t in (q, k, v, dout))
     qoff = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
     dq = torch.empty((B, H, N, dp), device=q.device, dtype=q.dtype)
     dk = torch.empty_like(dq)
     dv = torch.empty_like(dq)
-    a = _base_args(_lib.NON_SOFTMAX, q, is_causal, sm_scale, num_prefix, dp)
     a.q, a.k, a.v, a.dout = (_lib.tensor_desc(t) for t in (q_, k_, v_, do_))
     a.dq, a.dk, a.dv = (_lib.tensor_desc(t) for t in (dq, dk, dv))
     a.lse = qoff.data_ptr()
-    _launch("rbf_attn_bwd", a, q.device)
+    if pos_ is None:
+        _launch("rbf_attn_bwd", a, q.device)
+    else:
+        _launch_pos("rbf_attn_bwd_pos", a, pos_, q.device)
     return _unpad(dq, D), _unpad(dk, D), _unpad(dv, D)
 
 
@@ -306,8 +353,9 @@ def rbf_scaled_fwd_ex(
     sm_scale: float,
     num_prefix: int,
     token_major: bool = False,
+    pos: Optional[torch.Tensor] = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    return _softmax_fwd(q, k, v, is_causal, sm_scale, num_prefix, token_major)
+    return _softmax_fwd(q, k, v, is_causal, sm_scale, num_prefix, token_major, pos)
 
 
 def _fake_out(q: torch.Tensor, token_major: bool) -> torch.Tensor:
@@ -319,7 +367,7 @@ def _fake_out(q: torch.Tensor, token_major: bool) -> torch.Tensor:
 
 
 @rbf_scaled_fwd_ex.register_fake
-def _(q, k, v, is_causal, sm_scale, num_prefix, token_major=False):
+def _(q, k, v, is_causal, sm_scale, num_prefix, token_major=False, pos=None):
     B, H, N, _ = q.shape
     return _fake_out(q, token_major), torch.empty((B, H, N), device=q.device, dtype=torch.float32)
 
@@ -335,28 +383,39 @@ def rbf_scaled_bwd_ex(
     is_causal: bool,
     sm_scale: float,
     num_prefix: int,
+    pos: Optional[torch.Tensor] = None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    return _softmax_bwd(q, k, v, out, L, dout, is_causal, sm_scale, num_prefix)
+    return _softmax_bwd(q, k, v, out, L, dout, is_causal, sm_scale, num_prefix, pos)
 
 
 @rbf_scaled_bwd_ex.register_fake
-def _(q, k, v, out, L, dout, is_causal, sm_scale, num_prefix):
+def _(q, k, v, out, L, dout, is_causal, sm_scale, num_prefix, pos=None):
     return tuple(torch.empty_like(t, memory_format=torch.contiguous_format) for t in (q, k, v))
+
+
+def _pos_grad(pos, dq, dk):
+    """Gradient of the position term added to q and k: dq + dk, summed over
+    the batch when the term is shared by it."""
+    if pos is None:
+        return None
+    g = dq + dk
+    return g.sum(dim=0, keepdim=True) if pos.shape[0] == 1 and g.shape[0] != 1 else g
 
 
 def _scaled_ex_setup_context(ctx, inputs, output):
     q, k, v, is_causal, sm_scale, num_prefix = inputs[:6]
+    pos = inputs[7] if len(inputs) > 7 else None
     out, L = output
-    ctx.save_for_backward(q, k, v, out, L)
+    ctx.save_for_backward(q, k, v, out, L, pos)
     ctx.is_causal, ctx.sm_scale, ctx.num_prefix = is_causal, sm_scale, num_prefix
 
 
 def _scaled_ex_backward(ctx, dout, dL):
-    q, k, v, out, L = ctx.saved_tensors
+    q, k, v, out, L, pos = ctx.saved_tensors
     dq, dk, dv = torch.ops.rbf_attn_amd.scaled_bwd_ex(
-        q, k, v, out, L, dout, ctx.is_causal, ctx.sm_scale, ctx.num_prefix
+        q, k, v, out, L, dout, ctx.is_causal, ctx.sm_scale, ctx.num_prefix, pos
     )
-    return dq, dk, dv, None, None, None, None
+    return dq, dk, dv, None, None, None, None, _pos_grad(pos, dq, dk)
 
 
 torch.library.register_autograd(f"{_EX}::scaled_fwd_ex", _scaled_ex_backward, setup_context=_scaled_ex_setup_context)
@@ -371,12 +430,13 @@ def rbf_non_softmax_fwd_ex(
     sm_scale: float,
     num_prefix: int,
     token_major: bool = False,
+    pos: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    return _non_softmax_fwd(q, k, v, is_causal, sm_scale, num_prefix, token_major)
+    return _non_softmax_fwd(q, k, v, is_causal, sm_scale, num_prefix, token_major, pos)
 
 
 @rbf_non_softmax_fwd_ex.register_fake
-def _(q, k, v, is_causal, sm_scale, num_prefix, token_major=False):
+def _(q, k, v, is_causal, sm_scale, num_prefix, token_major=False, pos=None):
     return _fake_out(q, token_major)
 
 
@@ -389,27 +449,29 @@ def rbf_non_softmax_bwd_ex(
     is_causal: bool,
     sm_scale: float,
     num_prefix: int,
+    pos: Optional[torch.Tensor] = None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    return _non_softmax_bwd(q, k, v, dout, is_causal, sm_scale, num_prefix)
+    return _non_softmax_bwd(q, k, v, dout, is_causal, sm_scale, num_prefix, pos)
 
 
 @rbf_non_softmax_bwd_ex.register_fake
-def _(q, k, v, dout, is_causal, sm_scale, num_prefix):
+def _(q, k, v, dout, is_causal, sm_scale, num_prefix, pos=None):
     return tuple(torch.empty_like(t, memory_format=torch.contiguous_format) for t in (q, k, v))
 
 
 def _non_softmax_ex_setup_context(ctx, inputs, output):
     q, k, v, is_causal, sm_scale, num_prefix = inputs[:6]
-    ctx.save_for_backward(q, k, v)
+    pos = inputs[7] if len(inputs) > 7 else None
+    ctx.save_for_backward(q, k, v, pos)
     ctx.is_causal, ctx.sm_scale, ctx.num_prefix = is_causal, sm_scale, num_prefix
 
 
 def _non_softmax_ex_backward(ctx, dout):
-    q, k, v = ctx.saved_tensors
+    q, k, v, pos = ctx.saved_tensors
     dq, dk, dv = torch.ops.rbf_attn_amd.non_softmax_bwd_ex(
-        q, k, v, dout, ctx.is_causal, ctx.sm_scale, ctx.num_prefix
+        q, k, v, dout, ctx.is_causal, ctx.sm_scale, ctx.num_prefix, pos
     )
-    return dq, dk, dv, None, None, None, None
+    return dq, dk, dv, None, None, None, None, _pos_grad(pos, dq, dk)
 
 
 torch.library.register_autograd(
@@ -503,23 +565,29 @@ def rbf_decode(q, k_cache, v_cache, cache_lens=None, *, softmax=True, sm_scale=N
 # ---------------------------------------------------------------------------
 # Public wrappers (rbf_attention.py:848-853) and autograd.Function aliases.
 # ---------------------------------------------------------------------------
-def run_triton_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, token_major=False):
+def run_triton_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, token_major=False, pos=None):
     """Softmax RBF attention.  With the default ``sm_scale`` (1/sqrt(D)),
-    ``num_prefix=0`` and ``token_major=False`` this is exactly the reference's
-    ``run_triton_rbf``.  ``token_major=True`` returns the (B, H, N, D) output as
-    a view of a (B, N, H, D) buffer (see ``_alloc_out``)."""
-    if sm_scale is None and num_prefix == 0 and not token_major:
+    ``num_prefix=0``, ``token_major=False`` and no ``pos`` this is exactly the
+    reference's ``run_triton_rbf``.  ``token_major=True`` returns the
+    (B, H, N, D) output as a view of a (B, N, H, D) buffer (see
+    ``_alloc_out``).  ``pos`` (1 or B, H, N, D): attention of q + pos and
+    k + pos (the model's SuSiE embedding), fused into the kernels' Q/K reads
+    where the library supports it; its gradient is returned by autograd."""
+    if sm_scale is None and num_prefix == 0 and not token_major and pos is None:
         return torch.ops.rbf_attn_v5.scaled_fwd(q, k, v, is_causal)[0]
     scale = _default_scale(q) if sm_scale is None else float(sm_scale)
-    return torch.ops.rbf_attn_amd.scaled_fwd_ex(q, k, v, is_causal, scale, int(num_prefix), bool(token_major))[0]
+    return torch.ops.rbf_attn_amd.scaled_fwd_ex(q, k, v, is_causal, scale, int(num_prefix), bool(token_major), pos)[0]
 
 
-def run_triton_non_softmax_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, token_major=False):
-    """Non-softmax RBF attention, sum_j exp(-gamma||q_i-k_j||^2) v_j."""
-    if sm_scale is None and num_prefix == 0 and not token_major:
+def run_triton_non_softmax_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, token_major=False, pos=None):
+    """Non-softmax RBF attention, sum_j exp(-gamma||q_i-k_j||^2) v_j (pos as
+    in ``run_triton_rbf``)."""
+    if sm_scale is None and num_prefix == 0 and not token_major and pos is None:
         return torch.ops.rbf_attn_v5.non_softmax_fwd(q, k, v, is_causal)
     scale = _default_scale(q) if sm_scale is None else float(sm_scale)
-    return torch.ops.rbf_attn_amd.non_softmax_fwd_ex(q, k, v, is_causal, scale, int(num_prefix), bool(token_major))
+    return torch.ops.rbf_attn_amd.non_softmax_fwd_ex(
+        q, k, v, is_causal, scale, int(num_prefix), bool(token_major), pos
+    )
 
 
 class TritonRBFAttention(torch.autograd.Function):

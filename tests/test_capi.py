@@ -131,6 +131,30 @@ def test_empty_problem_is_noop(lib):
 
 
 # ---------------------------------------------------------------------------
+# position-term entry points (errors only: nothing here reaches a launch)
+# ---------------------------------------------------------------------------
+def test_pos_supported(lib):
+    def sup(**over):
+        return lib.rbf_attn_pos_supported(ctypes.byref(good_args(**over)))
+
+    assert sup(N=516) == 1 and sup(N=576, dtype=1) == 1 and sup(D=40) == 1
+    assert sup(dtype=2) == 0 and sup(D=128) == 0 and sup(D=32) == 0 and sup(N=577) == 0
+    assert sup(dtype=7) == -2 and sup(D=60) == -4
+
+
+def test_pos_entry_points_reject_before_launch(lib):
+    pos = _lib.Tensor(FAKE + 0x3000000, 0, 64 * 64, 64)
+    for fn in (lib.rbf_attn_fwd_pos, lib.rbf_attn_bwd_pos):
+        assert fn(ctypes.byref(good_args()), None, None) == -6
+        assert fn(ctypes.byref(good_args(D=128)), ctypes.byref(pos), None) == -8
+        assert "576" in lib.rbf_attn_last_error().decode()
+        assert fn(ctypes.byref(good_args(dtype=2)), ctypes.byref(pos), None) == -8
+        bad = _lib.Tensor(FAKE + 0x3000008, 0, 64 * 64, 64)
+        assert fn(ctypes.byref(good_args()), ctypes.byref(bad), None) == -3
+        assert fn(ctypes.byref(good_args(N=0)), ctypes.byref(pos), None) == 0
+
+
+# ---------------------------------------------------------------------------
 # decode entry points
 # ---------------------------------------------------------------------------
 def test_decode_struct_layout():

@@ -18,14 +18,18 @@ def small_cfg(**kw):
     return M.ModelConfig(**base)
 
 
-def math_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, token_major=False):
+def math_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, token_major=False, pos=None):
     assert num_prefix == 0
+    if pos is not None:
+        q, k = q + pos, k + pos
     g = sm_scale if sm_scale is not None else q.shape[-1] ** -0.5
     return math_path.softmax_math_forward(q.contiguous(), k.contiguous(), v.contiguous(), g, is_causal).to(q.dtype)
 
 
-def math_rbf_ns(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, token_major=False):
+def math_rbf_ns(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, token_major=False, pos=None):
     assert num_prefix == 0
+    if pos is not None:
+        q, k = q + pos, k + pos
     g = sm_scale if sm_scale is not None else q.shape[-1] ** -0.5
     return math_path.non_softmax_math_forward(q, k, v, g, is_causal).to(q.dtype)
 
