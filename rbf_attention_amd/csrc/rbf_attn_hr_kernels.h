@@ -87,6 +87,36 @@ __device__ inline void hr_neg_halfnorms(const T* sA, float* nrm, int rows, int o
   }
 }
 
+// Stores one token's 32 features of an accumulator tile (C layout: lane
+// (n, h) holds features fbase + 8(i/4) + 4h + i%4, i = 0..15, of token n) as
+// whole 16-byte chunks: lanes n and n + 32 trade halves of their 4-feature
+// groups (v_permlane32_swap), after which lane half h writes chunks 2j + h.
+// Every lane must call it (the swap reads the partner lane); `on` predicates
+// only the stores.  8-byte stores of the same data measured 2.3x the
+// compulsory HBM write bytes for the dK/dV tiles of the head-resident kernel.
+template <typename T>
+__device__ inline void store_tile_chunks(T* row, const float* v, int fbase, int h, int D, bool on) {
+  uint32_t w[8];
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int m = 0; m < 2; ++m) w[2 * g + m] = bits16<T>((T)v[4 * g + 2 * m]) | (bits16<T>((T)v[4 * g + 2 * m + 1]) << 16);
+#pragma unroll
+  for (int q = 0; q < 4; q += 2) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const auto r = __builtin_amdgcn_permlane32_swap(w[2 * q + m], w[2 * q + 2 + m], false, false);
+      w[2 * q + m] = r[0];
+      w[2 * q + 2 + m] = r[1];
+    }
+    const int f = fbase + 8 * (q + h);
+    if (on && f < D) {
+      const u32x4_t c = {w[2 * q], w[2 * q + 1], w[2 * q + 2], w[2 * q + 3]};
+      *reinterpret_cast<u32x4_t*>(row + f) = c;
+    }
+  }
+}
+
 // Block index of the k-th block (k = 0, 1, ...) of `wave` out of W, or -1:
 // blocks ranked heaviest first (rank 0 = block nblk-1 when `reverse`, i.e.
 // when the weight rises with the block index), dealt in snake order.
@@ -448,27 +478,26 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
 
     const float cs = xhalf_sum(csum);
     const int kb_next = hr_block(k + 1, wave, W, nblk, false);
-    if (ktok >= 0) {
-      T* dkrow = dK + (int64_t)ktok * p.sdk[2];
-      T* dvrow = dV + (int64_t)ktok * p.sdv[2];
-      const T* krow = K + (int64_t)ktok * p.sk[2];
+    const bool on = ktok >= 0;
+    T* dkrow = dK + (int64_t)ktok * p.sdk[2];
+    T* dvrow = dV + (int64_t)ktok * p.sdv[2];
+    const T* krow = K + (int64_t)ktok * p.sk[2];
 #pragma unroll
-      for (int d = 0; d < ND; ++d)
+    for (int d = 0; d < ND; ++d) {
+      float a[16];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int dd = 32 * d + 8 * g + 4 * h;
-          if (dd < D) {
-            float k4[4], a4[4], b4[4];
-            ld4fp<T>(krow + dd, Pos ? Pos + (int64_t)ktok * p.spos[2] + dd : nullptr, k4);
+      for (int g = 0; g < 4; ++g) {
+        const int dd = 32 * d + 8 * g + 4 * h;
+        float k4[4] = {0.f, 0.f, 0.f, 0.f};
+        if (on && dd < D) ld4fp<T>(krow + dd, Pos ? Pos + (int64_t)ktok * p.spos[2] + dd : nullptr, k4);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              a4[e] = g2 * (dkacc[d][4 * g + e] - cs * k4[e]);
-              b4[e] = dvacc[d][4 * g + e];
-            }
-            st4f<T>(dkrow + dd, a4);
-            st4f<T>(dvrow + dd, b4);
-          }
-        }
+        for (int e = 0; e < 4; ++e) a[4 * g + e] = g2 * (dkacc[d][4 * g + e] - cs * k4[e]);
+      }
+      float bv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) bv[i] = dvacc[d][i];
+      store_tile_chunks<T>(dkrow, a, 32 * d, h, D, on);
+      store_tile_chunks<T>(dvrow, bv, 32 * d, h, D, on);
     }
     kb = kb_next;
     if (kb >= 0) load_kv(kb);
