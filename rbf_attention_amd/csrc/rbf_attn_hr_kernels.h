@@ -117,6 +117,34 @@ __device__ inline void store_tile_chunks(T* row, const float* v, int fbase, int 
   }
 }
 
+// The lane's token features in the accumulator layout of a 32x32 tile whose
+// rows are features (lane (n, h) of tile d holds features 32d + 8g + 4h + e,
+// g, e = 0..3), taken from B-operand fragments of the same token (f[t] of
+// lane (n, h) = features 16t + 8h .. 16t + 8h + 7).  Lane halves trade
+// dwords with v_permlane32_swap: out[d][g][e] for features 32d + 8g + 4h + e.
+// Every lane must call it.
+template <typename T, int KS>
+__device__ inline void frag_cfeat(const typename Elem<T>::frag* f, float (*out)[4][4]) {
+  typedef typename Elem<T>::raw raw;
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    const raw w = __builtin_bit_cast(raw, f[t]);
+    // (w0, w2) -> features 4h + {0, 1} of groups g = 2(t%2) and 2(t%2) + 1;
+    // (w1, w3) -> features 4h + {2, 3}
+    const auto a = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      float* o = out[t >> 1][2 * (t & 1) + s];
+      const uint32_t lo = a[s], hi = b[s];
+      o[0] = (float)__builtin_bit_cast(T, (uint16_t)(lo & 0xffffu));
+      o[1] = (float)__builtin_bit_cast(T, (uint16_t)(lo >> 16));
+      o[2] = (float)__builtin_bit_cast(T, (uint16_t)(hi & 0xffffu));
+      o[3] = (float)__builtin_bit_cast(T, (uint16_t)(hi >> 16));
+    }
+  }
+}
+
 // Block index of the k-th block (k = 0, 1, ...) of `wave` out of W, or -1:
 // blocks ranked heaviest first (rank 0 = block nblk-1 when `reverse`, i.e.
 // when the weight rises with the block index), dealt in snake order.
@@ -382,12 +410,11 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
   const float* offg = p.lse + (int64_t)bh * N;
   const float* delg = SOFTMAX ? p.delta + (int64_t)bh * N : nullptr;
 
-  // K, V and -c 0.5||k||^2 of one key block, straight to registers.
+  // K and V of one key block, straight to registers (their norm is taken
+  // where the block is first used, so the loads stay in flight until then).
   frag kf[KS], vf[KS];
-  float nckn = 0.f;
   auto load_kv = [&](int kb) {
     const int ktok = org + 32 * kb + n;
-    float ss = 0.f;
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
       const bool ok = kb >= 0 && ktok >= 0 && 16 * t + 8 * h < D;
@@ -395,25 +422,44 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
                            Pos ? Pos + (int64_t)ktok * p.spos[2] + 16 * t + 8 * h : nullptr)
                  : zero_frag<T>();
       vf[t] = ok ? ld8<T>(V + (int64_t)ktok * p.sv[2] + 16 * t + 8 * h) : zero_frag<T>();
-      ss += sumsq8<T>(kf[t]);
     }
-    nckn = -c * 0.5f * xhalf_sum(ss);
   };
   int kb = hr_block(0, wave, W, nblk, false);
   load_kv(kb);
 
+  // L and Delta of the rows this thread stages are requested with the Q / dO
+  // rows, so the load phase waits for one round trip.
+  constexpr int RPT = (ROWS + NT - 1) / NT;
+  float offv[RPT], delv[RPT];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int r = tid + j * NT, tok = org + r;
+    const bool ok = r < 32 * nblk && tok >= 0 && tok < N;
+    offv[j] = ok ? offg[tok] : 0.f;
+    delv[j] = (SOFTMAX && ok) ? delg[tok] : 0.f;
+  }
   hr_load2<T, ROWS, DP, NT>(Q, p.sq[2], sQ, dO, p.sdo[2], sD, 32 * nblk, org, N, D, tid, Pos, p.spos[2]);
-  for (int r = tid; r < 32 * nblk; r += NT) {
-    const int tok = org + r;
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int r = tid + j * NT, tok = org + r;
     const bool ok = tok >= 0 && tok < N;
-    sOff[r] = ok ? -offg[tok] * inv_c : -__builtin_inff();  // padding queries: P = 0
-    sDel[r] = (SOFTMAX && ok) ? -delg[tok] : 0.f;
+    if (r < 32 * nblk) {
+      sOff[r] = ok ? -offv[j] * inv_c : -__builtin_inff();  // padding queries: P = 0
+      sDel[r] = ok ? -delv[j] : 0.f;
+    }
   }
   __syncthreads();
 
   const float g2 = 2.f * p.gamma;
   for (int k = 0; kb >= 0; ++k) {
     const int k0 = org + 32 * kb, ktok = k0 + n;
+    float nckn;  // -c 0.5 ||k||^2
+    {
+      float ss = 0.f;
+#pragma unroll
+      for (int t = 0; t < KS; ++t) ss += sumsq8<T>(kf[t]);
+      nckn = -c * 0.5f * xhalf_sum(ss);
+    }
     const int ilo = first_query(ktok, causal, npre);
     // query blocks [qb0, nblk) hold every query that sees some key of the block
     const int qlo = causal ? (max(k0, 0) < npre ? 0 : max(k0, 0)) : 0;
@@ -477,30 +523,29 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
     }
 
     const float cs = xhalf_sum(csum);
-    const int kb_next = hr_block(k + 1, wave, W, nblk, false);
+    // The block's K (with the position term) in the dK accumulator layout,
+    // for the key-norm term; then the next block's K and V are requested
+    // before this block's results are written.
+    float kc[ND][4][4];
+    frag_cfeat<T, KS>(kf, kc);
+    kb = hr_block(k + 1, wave, W, nblk, false);
+    if (kb >= 0) load_kv(kb);
     const bool on = ktok >= 0;
     T* dkrow = dK + (int64_t)ktok * p.sdk[2];
     T* dvrow = dV + (int64_t)ktok * p.sdv[2];
-    const T* krow = K + (int64_t)ktok * p.sk[2];
 #pragma unroll
     for (int d = 0; d < ND; ++d) {
       float a[16];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int dd = 32 * d + 8 * g + 4 * h;
-        float k4[4] = {0.f, 0.f, 0.f, 0.f};
-        if (on && dd < D) ld4fp<T>(krow + dd, Pos ? Pos + (int64_t)ktok * p.spos[2] + dd : nullptr, k4);
+      for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) a[4 * g + e] = g2 * (dkacc[d][4 * g + e] - cs * k4[e]);
-      }
+        for (int e = 0; e < 4; ++e) a[4 * g + e] = g2 * (dkacc[d][4 * g + e] - cs * kc[d][g][e]);
       float bv[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) bv[i] = dvacc[d][i];
       store_tile_chunks<T>(dkrow, a, 32 * d, h, D, on);
       store_tile_chunks<T>(dvrow, bv, 32 * d, h, D, on);
     }
-    kb = kb_next;
-    if (kb >= 0) load_kv(kb);
   }
 }
 
@@ -543,7 +588,10 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
   const T* dO = reinterpret_cast<const T*>(p.dout) + b * p.sdo[0] + hh * p.sdo[1];
   T* dQ = reinterpret_cast<T*>(p.dq) + b * p.sdq[0] + hh * p.sdq[1];
 
-  // Q and dO fragments of one query block, straight to registers.
+  // Q and dO fragments of one query block, straight to registers; the next
+  // block's are requested before this block's dQ is written.  (The block's O
+  // rows and L are read where Delta is formed: requested together with Q and
+  // dO they cost registers and measured 1.5 us slower at C2.)
   frag qf[KS], df[KS];
   auto load_qd = [&](int qb) {
     const int qtok = org + 32 * qb + n;
@@ -575,8 +623,8 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
 #pragma unroll
       for (int t = 0; t < KS; ++t) {
         const bool ok = qvalid && 16 * t + 8 * h < D;
-        const frag of = ok ? ld8<T>(Og + (int64_t)qtok * p.so[2] + 16 * t + 8 * h) : zero_frag<T>();
-        sdot += dot8<T>(of, df[t]);
+        const frag o1 = ok ? ld8<T>(Og + (int64_t)qtok * p.so[2] + 16 * t + 8 * h) : zero_frag<T>();
+        sdot += dot8<T>(o1, df[t]);
       }
       dlt = xhalf_sum(sdot);
       off = qvalid ? p.lse[(int64_t)bh * N + qtok] : 0.f;
@@ -638,10 +686,15 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
 
     float rs = 0.f;
     if constexpr (!SOFTMAX) rs = xhalf_sum(rsum);
-    const int qb_next = hr_block(k + 1, wave, W, nblk, causal);
+    // Non-softmax: the block's Q (with the position term) in the dQ
+    // accumulator layout, for the norm term.  Then the next block's operands
+    // are requested before this block's dQ is written.
+    float qc[SOFTMAX ? 1 : ND][4][4];
+    if constexpr (!SOFTMAX) frag_cfeat<T, KS>(qf, qc);
+    qb = hr_block(k + 1, wave, W, nblk, causal);
+    if (qb >= 0) load_qd(qb);
     if (qvalid) {
       T* drow = dQ + (int64_t)qtok * p.sdq[2];
-      const T* qrow = Q + (int64_t)qtok * p.sq[2];
 #pragma unroll
       for (int d = 0; d < ND; ++d)
 #pragma unroll
@@ -649,21 +702,15 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
           const int dd = 32 * d + 8 * g + 4 * h;
           if (dd < D) {
             float v4[4];
-            if constexpr (SOFTMAX) {
 #pragma unroll
-              for (int e = 0; e < 4; ++e) v4[e] = g2 * dqacc[d][4 * g + e];
-            } else {
-              float q4[4];
-              ld4fp<T>(qrow + dd, Pos ? Pos + (int64_t)qtok * p.spos[2] + dd : nullptr, q4);
-#pragma unroll
-              for (int e = 0; e < 4; ++e) v4[e] = g2 * (dqacc[d][4 * g + e] - rs * q4[e]);
+            for (int e = 0; e < 4; ++e) {
+              if constexpr (SOFTMAX) v4[e] = g2 * dqacc[d][4 * g + e];
+              else v4[e] = g2 * (dqacc[d][4 * g + e] - rs * qc[d][g][e]);
             }
             st4f<T>(drow + dd, v4);
           }
         }
     }
-    qb = qb_next;
-    if (qb >= 0) load_qd(qb);
   }
 }
 

@@ -22,6 +22,21 @@ RBF_DECLARE_LAUNCHERS(fp32)
 
 #undef RBF_DECLARE_LAUNCHERS
 
+// Head-resident kernels (16-bit elements, 32 < D <= 64, N <= 32 * kHrMaxBlocks;
+// defined in rbf_attn_launch_hr.hip).  They return hipErrorInvalidValue for
+// shapes they do not cover.
+constexpr int kHrMaxBlocks = 18;
+
+#define RBF_DECLARE_HR_LAUNCHERS(NAME)                                                         \
+  hipError_t launch_fwd_hr_##NAME(const Params& p, int variant, int waves, hipStream_t st);   \
+  hipError_t launch_bwd_dq_hr_##NAME(const Params& p, int variant, hipStream_t st);           \
+  hipError_t launch_bwd_dkdv_hr_##NAME(const Params& p, int variant, hipStream_t st);
+
+RBF_DECLARE_HR_LAUNCHERS(bf16)
+RBF_DECLARE_HR_LAUNCHERS(fp16)
+
+#undef RBF_DECLARE_HR_LAUNCHERS
+
 // Decode split geometry: waves per work-group (one 32-key block each per
 // tile); fp32 tiles need twice the LDS, so fp32 runs half as many.
 inline int decode_waves(int dtype_is_fp32) { return dtype_is_fp32 ? 2 : 4; }

@@ -9,7 +9,6 @@
 // (an index into the candidate lists below) for tuning sweeps.
 #include <stdlib.h>
 
-#include "rbf_attn_hr_kernels.h"
 #include "rbf_attn_kernels.h"
 #include "rbf_attn_launch.h"
 #include "rbf_decode_kernels.h"
@@ -95,25 +94,36 @@ hipError_t launch(F kernel, const Params& p, int blocks_per_wg, int threads, int
   return hipGetLastError();
 }
 
-template <int DP, bool SM, int W, int NB, bool POS = false>
-hipError_t fwd_hr_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_fwd_hr_kernel<Elt, DP, W, NB, SM, POS>), dim3((unsigned)((long long)p.B * p.H)), dim3(64 * W), 0,
-                     st, p);
-  return hipGetLastError();
+// Head-resident launchers of this element type (rbf_attn_launch_hr.hip);
+// never reached for fp32.
+hipError_t hr_fwd(const Params& p, bool sm, int waves, hipStream_t st) {
+#if RBF_ELEM_ID == 0
+  return launch_fwd_hr_bf16(p, sm ? 0 : 1, waves, st);
+#elif RBF_ELEM_ID == 1
+  return launch_fwd_hr_fp16(p, sm ? 0 : 1, waves, st);
+#else
+  return hipErrorInvalidValue;
+#endif
 }
 
-template <int DP, bool SM, int W, int NB, bool POS = false>
-hipError_t dq_hr_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_bwd_dq_hr_kernel<Elt, DP, W, NB, SM, POS>), dim3((unsigned)((long long)p.B * p.H)), dim3(64 * W),
-                     0, st, p);
-  return hipGetLastError();
+hipError_t hr_dq(const Params& p, bool sm, hipStream_t st) {
+#if RBF_ELEM_ID == 0
+  return launch_bwd_dq_hr_bf16(p, sm ? 0 : 1, st);
+#elif RBF_ELEM_ID == 1
+  return launch_bwd_dq_hr_fp16(p, sm ? 0 : 1, st);
+#else
+  return hipErrorInvalidValue;
+#endif
 }
 
-template <int DP, bool SM, int W, int NB, bool POS = false>
-hipError_t dkdv_hr_cfg(const Params& p, hipStream_t st) {
-  hipLaunchKernelGGL((rbf_bwd_dkdv_hr_kernel<Elt, DP, W, NB, SM, POS>), dim3((unsigned)((long long)p.B * p.H)),
-                     dim3(64 * W), 0, st, p);
-  return hipGetLastError();
+hipError_t hr_dkdv(const Params& p, bool sm, hipStream_t st) {
+#if RBF_ELEM_ID == 0
+  return launch_bwd_dkdv_hr_bf16(p, sm ? 0 : 1, st);
+#elif RBF_ELEM_ID == 1
+  return launch_bwd_dkdv_hr_fp16(p, sm ? 0 : 1, st);
+#else
+  return hipErrorInvalidValue;
+#endif
 }
 
 // Head-resident kernels (16-bit): the head's nblk blocks fit the kernel's LDS
@@ -132,7 +142,7 @@ bool use_hr(const Params& p, int nb_max, int which) {
   if (forced > 0) return true;
   return (long long)p.B * p.H >= cu_count();
 }
-constexpr int kHrBlocks64 = 18;  // D <= 64: N <= 576
+constexpr int kHrBlocks64 = kHrMaxBlocks;  // D <= 64: N <= 576
 
 template <int DP, bool SM, int W, int BN, bool BIN = false>
 hipError_t fwd_cfg(const Params& p, hipStream_t st) {
@@ -177,12 +187,12 @@ template <int DP, bool SM>
 hipError_t fwd_default(const Params& p, hipStream_t st) {
   if (p.pos) {
     if constexpr (!kIsF32 && DP == 64) {
-      if (p.nblk <= kHrBlocks64) return fwd_hr_cfg<DP, SM, 12, kHrBlocks64, true>(p, st);
+      if (p.nblk <= kHrBlocks64) return hr_fwd(p, SM, 12, st);
     }
     return hipErrorInvalidValue;
   }
   if constexpr (!kIsF32 && DP == 64) {
-    if (use_hr(p, kHrBlocks64, 1)) return fwd_hr_cfg<DP, SM, 12, kHrBlocks64>(p, st);
+    if (use_hr(p, kHrBlocks64, 1)) return hr_fwd(p, SM, 12, st);
   }
   if constexpr (kIsF32) return fwd_cfg<DP, SM, 4, 32>(p, st);
   else if constexpr (DP <= 64) {
@@ -197,12 +207,12 @@ template <int DP, bool SM>
 hipError_t dq_default(const Params& p, hipStream_t st) {
   if (p.pos) {
     if constexpr (!kIsF32 && DP == 64) {
-      if (p.nblk <= kHrBlocks64) return dq_hr_cfg<DP, SM, 8, kHrBlocks64, true>(p, st);
+      if (p.nblk <= kHrBlocks64) return hr_dq(p, SM, st);
     }
     return hipErrorInvalidValue;
   }
   if constexpr (!kIsF32 && DP == 64) {
-    if (use_hr(p, kHrBlocks64, 2)) return dq_hr_cfg<DP, SM, 8, kHrBlocks64>(p, st);
+    if (use_hr(p, kHrBlocks64, 2)) return hr_dq(p, SM, st);
   }
   if constexpr (kIsF32) return dq_cfg<DP, SM, 4, 1, 32>(p, st);
   else if constexpr (DP <= 64)
@@ -215,12 +225,12 @@ template <int DP, bool SM>
 hipError_t dkdv_default(const Params& p, hipStream_t st) {
   if (p.pos) {
     if constexpr (!kIsF32 && DP == 64) {
-      if (p.nblk <= kHrBlocks64) return dkdv_hr_cfg<DP, SM, 8, kHrBlocks64, true>(p, st);
+      if (p.nblk <= kHrBlocks64) return hr_dkdv(p, SM, st);
     }
     return hipErrorInvalidValue;
   }
   if constexpr (!kIsF32 && DP == 64) {
-    if (use_hr(p, kHrBlocks64, 4)) return dkdv_hr_cfg<DP, SM, 8, kHrBlocks64>(p, st);
+    if (use_hr(p, kHrBlocks64, 4)) return hr_dkdv(p, SM, st);
   }
   if constexpr (kIsF32) return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
   else if constexpr (DP <= 64) {
@@ -249,10 +259,10 @@ hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
     case 4: return fwd_cfg<DP, SM, 2, 64>(p, st);
     case 5: return fwd_cfg<DP, SM, 4, 32>(p, st);
     case 10:
-      if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return fwd_hr_cfg<DP, SM, 8, kHrBlocks64>(p, st); }
+      if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return hr_fwd(p, SM, 8, st); }
       break;
     case 11:
-      if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return fwd_hr_cfg<DP, SM, 12, kHrBlocks64>(p, st); }
+      if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return hr_fwd(p, SM, 12, st); }
       break;
     default: break;
   }
