@@ -42,10 +42,14 @@ COMMON_FLAGS = [
 ]
 
 
-# The head-resident kernels (short heads held in LDS, one work-group per head)
-# measured 3-5 % faster with the ILP-maximising machine scheduler; the
-# streaming kernels measured slower with it, so only their unit takes it.
+# Machine-scheduler strategy per unit, chosen by measurement on MI355X: the
+# head-resident kernels (short heads held in LDS, one work-group per head)
+# run 3-5 % faster with the ILP-maximising scheduler, which slows the
+# long-sequence streaming dQ by 15 %; the streaming kernels run 1-2.5 %
+# faster with the iterative ILP scheduler (C3 5.74 -> 5.65 ms, C4 495 ->
+# 487 us per step).
 HR_FLAGS = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
+STREAM_FLAGS = ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
 
 
 def _hipcc() -> str:
@@ -67,9 +71,9 @@ def build(verbose: bool = True) -> str:
     hipcc = _hipcc()
     units = [
         ("rbf_attn_capi.hip", []),
-        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=0"]),
-        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=1"]),
-        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=2"]),
+        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=0", *STREAM_FLAGS]),
+        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=1", *STREAM_FLAGS]),
+        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=2", *STREAM_FLAGS]),
         ("rbf_attn_launch_hr.hip", ["-DRBF_ELEM_ID=0", *HR_FLAGS]),
         ("rbf_attn_launch_hr.hip", ["-DRBF_ELEM_ID=1", *HR_FLAGS]),
     ]
