@@ -174,6 +174,14 @@ __global__ __launch_bounds__(64 * W) void rbf_decode_split_kernel(const DecodePa
   }
 }
 
+// Max / sum over the 64 lanes of a wave (every lane receives the result).
+__device__ inline float wave_max64(float x) {
+  x = xhalf_max(x);
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
 template <typename T, int DP, bool SOFTMAX>
 __global__ __launch_bounds__(64) void rbf_decode_merge_kernel(const DecodeParams p) {
   const int lane = threadIdx.x;
@@ -185,21 +193,35 @@ __global__ __launch_bounds__(64) void rbf_decode_merge_kernel(const DecodeParams
   const float* wo = p.ws + (int64_t)bh * P * Tq * DP;
   const float* wm = p.ws + (int64_t)p.B * p.H * P * Tq * DP + (int64_t)bh * P * Tq;
   const float* wl = wm + (int64_t)p.B * p.H * P * Tq;
+  // M = max_p m_p, the lanes striding over the partials
   float M = -__builtin_inff();
-  for (int q = 0; q < P; ++q) M = fmaxf(M, wm[q * Tq + t]);
-  constexpr int PER = (DP + 63) / 64;
+  for (int q = lane; q < P; q += 64) M = fmaxf(M, wm[q * Tq + t]);
+  M = wave_max64(M);
+  // O and l: partials are read G at a time, so that their loads overlap
+  constexpr int PER = (DP + 63) / 64, G = 8;
   float acc[PER] = {};
   float l = 0.f;
-  for (int q = 0; q < P; ++q) {
-    const float mq = wm[q * Tq + t];
-    float w;
-    if constexpr (SOFTMAX) w = (mq == -__builtin_inff()) ? 0.f : fast_exp2(mq - M);
-    else w = 1.f;
-    if constexpr (SOFTMAX) l = fmaf(w, wl[q * Tq + t], l);
+  for (int q0 = 0; q0 < P; q0 += G) {
+    float w[G], lq[G], ov[G][PER];
 #pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      const int d = lane + 64 * e;
-      if (d < DP) acc[e] = fmaf(w, wo[((int64_t)q * Tq + t) * DP + d], acc[e]);
+    for (int j = 0; j < G; ++j) {
+      const int q = q0 + j;
+      const bool ok = q < P;
+      const float mq = ok ? wm[q * Tq + t] : -__builtin_inff();
+      if constexpr (SOFTMAX) w[j] = (mq == -__builtin_inff()) ? 0.f : fast_exp2(mq - M);
+      else w[j] = ok ? 1.f : 0.f;
+      lq[j] = (SOFTMAX && ok) ? wl[q * Tq + t] : 0.f;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const int d = lane + 64 * e;
+        ov[j][e] = (ok && d < DP) ? wo[((int64_t)q * Tq + t) * DP + d] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if constexpr (SOFTMAX) l = fmaf(w[j], lq[j], l);
+#pragma unroll
+      for (int e = 0; e < PER; ++e) acc[e] = fmaf(w[j], ov[j][e], acc[e]);
     }
   }
   const float inv = SOFTMAX ? (l > 0.f ? 1.f / l : 0.f) : 1.f;
