@@ -23,6 +23,15 @@
 
 namespace rbf {
 
+// A position term is added where the value is consumed, not where it is
+// loaded: a sum taken right after the loads makes them wait there, which
+// turns the prefetch of the next block into a synchronous load.
+template <typename T, bool POS>
+__device__ inline void add_pos(typename Elem<T>::frag* x, const typename Elem<T>::frag* pos, int n) {
+  if constexpr (POS)
+    for (int i = 0; i < n; ++i) x[i] = add8<T>(x[i], pos[i]);
+}
+
 // Chunk-major index of unit u: 16 consecutive units cover 4 tokens x 4
 // chunks, i.e. 64 contiguous bytes of each of 4 rows in global memory.
 template <int DP>
@@ -35,20 +44,20 @@ __device__ inline void hr_unit(int u, int& row, int& ch) {
 
 // Loads rows [0, rows) -- tokens org + row -- of two (N, D) slices into
 // chunk-major LDS tiles of ROWS rows; tokens outside [0, N) and features
-// >= D are zero; addA (row stride asa), when not null, is added to every row
-// of the first slice (position term).  Every chunk of a thread is requested
+// >= D are zero; when ADD, addA (row stride asa) is added to every row of the
+// first slice (position term).  Every chunk of a thread is requested
 // before the first is
 // stored.  The code is branch-free: with conditional stores here the compiler's
 // wait-count insertion no longer tells later LDS reads of other tiles apart
 // from outstanding LDS-DMA loads, and makes them wait for those loads.
-template <typename T, int ROWS, int DP, int NT>
+template <typename T, int ROWS, int DP, int NT, bool ADD>
 __device__ inline void hr_load2(const T* A, int64_t sa, T* sA, const T* B, int64_t sb, T* sB, int rows, int org,
-                                int N, int D, int tid, const T* addA = nullptr, int64_t asa = 0) {
+                                int N, int D, int tid, const T* addA, int64_t asa) {
   typedef typename Elem<T>::frag frag;
   typedef CLayout<ROWS> L;
   constexpr int PB = (ROWS * (DP / 8) + NT - 1) / NT;
   const int units = rows * (DP / 8);
-  frag ra[PB], rb[PB];
+  frag ra[PB], rb[PB], rp[ADD ? PB : 1];
 #pragma unroll
   for (int j = 0; j < PB; ++j) {
     const int u = tid + j * NT;
@@ -56,10 +65,11 @@ __device__ inline void hr_load2(const T* A, int64_t sa, T* sA, const T* B, int64
     hr_unit<DP>(u, row, ch);
     const int tok = org + row;
     const bool ok = u < units && tok >= 0 && tok < N && ch * 8 < D;
-    ra[j] = ok ? ld8p<T>(A + (int64_t)tok * sa + ch * 8, addA ? addA + (int64_t)tok * asa + ch * 8 : nullptr)
-               : zero_frag<T>();
+    ra[j] = ok ? ld8<T>(A + (int64_t)tok * sa + ch * 8) : zero_frag<T>();
     rb[j] = ok ? ld8<T>(B + (int64_t)tok * sb + ch * 8) : zero_frag<T>();
+    if constexpr (ADD) rp[j] = ok ? ld8<T>(addA + (int64_t)tok * asa + ch * 8) : zero_frag<T>();
   }
+  add_pos<T, ADD>(ra, rp, PB);
   // Units past the tile store into the padding after chunk column 0 instead
   // of branching around the store.
 #pragma unroll
@@ -194,24 +204,27 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
   const T* V = reinterpret_cast<const T*>(p.v) + b * p.sv[0] + hh * p.sv[1];
   T* O = reinterpret_cast<T*>(const_cast<void*>(p.o)) + b * p.so[0] + hh * p.so[1];
 
-  auto load_q = [&](int qb, frag* qf) {
+  // Q fragments of a query block (and the position term's, summed with
+  // them where they are consumed)
+  auto load_q = [&](int qb, frag* qf, frag* pf) {
     const int qtok = org + 32 * qb + n;
 #pragma unroll
-    for (int t = 0; t < KS; ++t)
-      qf[t] = (qb >= 0 && qtok >= 0 && 16 * t + 8 * h < D)
-                  ? ld8p<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h,
-                            Pos ? Pos + (int64_t)qtok * p.spos[2] + 16 * t + 8 * h : nullptr)
-                  : zero_frag<T>();
+    for (int t = 0; t < KS; ++t) {
+      const bool ok = qb >= 0 && qtok >= 0 && 16 * t + 8 * h < D;
+      qf[t] = ok ? ld8<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h) : zero_frag<T>();
+      if constexpr (POS) pf[t] = ok ? ld8<T>(Pos + (int64_t)qtok * p.spos[2] + 16 * t + 8 * h) : zero_frag<T>();
+    }
   };
   // The first query block's Q fragments are requested before the K/V load.
-  frag qf[KS];
+  frag qf[KS], pq[POS ? KS : 1];
   int qb = hr_block(0, wave, W, nblk, causal);
-  load_q(qb, qf);
+  load_q(qb, qf, pq);
 
-  hr_load2<T, ROWS, DP, NT>(K, p.sk[2], sK, V, p.sv[2], sV, 32 * nblk, org, N, D, tid, Pos, p.spos[2]);
+  hr_load2<T, ROWS, DP, NT, POS>(K, p.sk[2], sK, V, p.sv[2], sV, 32 * nblk, org, N, D, tid, Pos, p.spos[2]);
   __syncthreads();
   hr_neg_halfnorms<T, ROWS, DP, NT>(sK, sKn, 32 * nblk, org, N, tid);
   __syncthreads();
+  add_pos<T, POS>(qf, pq, KS);
 
   auto load_k = [&](int kb, frag* kA) {
 #pragma unroll
@@ -233,8 +246,8 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
   for (int k = 0; qb >= 0; ++k) {
     // the next block's Q fragments are requested before this block's work
     const int qb_next = hr_block(k + 1, wave, W, nblk, causal);
-    frag qf_next[KS];
-    load_q(qb_next, qf_next);
+    frag qf_next[KS], pq_next[POS ? KS : 1];
+    load_q(qb_next, qf_next, pq_next);
     const int q0 = org + 32 * qb, qtok = q0 + n;
     const bool qvalid = qtok >= 0;
     const int jmax = last_key(qtok, N, causal, npre);
@@ -364,6 +377,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
     qb = qb_next;
 #pragma unroll
     for (int t = 0; t < KS; ++t) qf[t] = qf_next[t];
+    add_pos<T, POS>(qf, pq_next, KS);
   }
 }
 
@@ -412,16 +426,15 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
 
   // K and V of one key block, straight to registers (their norm is taken
   // where the block is first used, so the loads stay in flight until then).
-  frag kf[KS], vf[KS];
+  frag kf[KS], vf[KS], pk[POS ? KS : 1];
   auto load_kv = [&](int kb) {
     const int ktok = org + 32 * kb + n;
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
       const bool ok = kb >= 0 && ktok >= 0 && 16 * t + 8 * h < D;
-      kf[t] = ok ? ld8p<T>(K + (int64_t)ktok * p.sk[2] + 16 * t + 8 * h,
-                           Pos ? Pos + (int64_t)ktok * p.spos[2] + 16 * t + 8 * h : nullptr)
-                 : zero_frag<T>();
+      kf[t] = ok ? ld8<T>(K + (int64_t)ktok * p.sk[2] + 16 * t + 8 * h) : zero_frag<T>();
       vf[t] = ok ? ld8<T>(V + (int64_t)ktok * p.sv[2] + 16 * t + 8 * h) : zero_frag<T>();
+      if constexpr (POS) pk[t] = ok ? ld8<T>(Pos + (int64_t)ktok * p.spos[2] + 16 * t + 8 * h) : zero_frag<T>();
     }
   };
   int kb = hr_block(0, wave, W, nblk, false);
@@ -438,7 +451,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
     offv[j] = ok ? offg[tok] : 0.f;
     delv[j] = (SOFTMAX && ok) ? delg[tok] : 0.f;
   }
-  hr_load2<T, ROWS, DP, NT>(Q, p.sq[2], sQ, dO, p.sdo[2], sD, 32 * nblk, org, N, D, tid, Pos, p.spos[2]);
+  hr_load2<T, ROWS, DP, NT, POS>(Q, p.sq[2], sQ, dO, p.sdo[2], sD, 32 * nblk, org, N, D, tid, Pos, p.spos[2]);
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int r = tid + j * NT, tok = org + r;
@@ -453,6 +466,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
   const float g2 = 2.f * p.gamma;
   for (int k = 0; kb >= 0; ++k) {
     const int k0 = org + 32 * kb, ktok = k0 + n;
+    add_pos<T, POS>(kf, pk, KS);
     float nckn;  // -c 0.5 ||k||^2
     {
       float ss = 0.f;
@@ -592,28 +606,28 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
   // block's are requested before this block's dQ is written.  (The block's O
   // rows and L are read where Delta is formed: requested together with Q and
   // dO they cost registers and measured 1.5 us slower at C2.)
-  frag qf[KS], df[KS];
+  frag qf[KS], df[KS], pq[POS ? KS : 1];
   auto load_qd = [&](int qb) {
     const int qtok = org + 32 * qb + n;
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
       const bool ok = qb >= 0 && qtok >= 0 && 16 * t + 8 * h < D;
-      qf[t] = ok ? ld8p<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h,
-                           Pos ? Pos + (int64_t)qtok * p.spos[2] + 16 * t + 8 * h : nullptr)
-                 : zero_frag<T>();
+      qf[t] = ok ? ld8<T>(Q + (int64_t)qtok * p.sq[2] + 16 * t + 8 * h) : zero_frag<T>();
       df[t] = ok ? ld8<T>(dO + (int64_t)qtok * p.sdo[2] + 16 * t + 8 * h) : zero_frag<T>();
+      if constexpr (POS) pq[t] = ok ? ld8<T>(Pos + (int64_t)qtok * p.spos[2] + 16 * t + 8 * h) : zero_frag<T>();
     }
   };
   int qb = hr_block(0, wave, W, nblk, causal);
   load_qd(qb);
 
-  hr_load2<T, ROWS, DP, NT>(K, p.sk[2], sK, V, p.sv[2], sV, 32 * nblk, org, N, D, tid, Pos, p.spos[2]);
+  hr_load2<T, ROWS, DP, NT, POS>(K, p.sk[2], sK, V, p.sv[2], sV, 32 * nblk, org, N, D, tid, Pos, p.spos[2]);
   __syncthreads();
   hr_neg_halfnorms<T, ROWS, DP, NT>(sK, sKn, 32 * nblk, org, N, tid);
   __syncthreads();
 
   const float g2 = 2.f * p.gamma;
   for (int k = 0; qb >= 0; ++k) {
+    add_pos<T, POS>(qf, pq, KS);
     const int q0 = org + 32 * qb, qtok = q0 + n;
     const bool qvalid = qtok >= 0;
     const int jmax = last_key(qtok, N, causal, npre);

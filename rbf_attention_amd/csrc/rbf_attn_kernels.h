@@ -159,6 +159,16 @@ __device__ inline typename Elem<T>::frag ld8p(const T* p, const T* pp) {
   return pp ? add8<T>(x, ld8<T>(pp)) : x;
 }
 
+// ld8 of p, plus the 8 elements at pp (rounded as add8) when ADD: a position
+// term fused into a Q or K read, chosen at compile time so that the loads
+// carry no null-pointer branches (with them every load waited on the
+// previous one).
+template <typename T, bool ADD>
+__device__ inline typename Elem<T>::frag ld8a(const T* p, const T* pp) {
+  if constexpr (ADD) return add8<T>(ld8<T>(p), ld8<T>(pp));
+  else return ld8<T>(p);
+}
+
 // 4 consecutive elements (8-byte aligned for 16-bit types, 16 for fp32).
 template <typename T>
 __device__ inline void ld4f(const T* p, float out[4]) {

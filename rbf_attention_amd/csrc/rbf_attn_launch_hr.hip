@@ -58,11 +58,14 @@ bool fits(const Params& p) { return p.D > 32 && p.D <= DP && p.nblk <= NB; }
 #define RBF_CAT(a, b) RBF_CAT2(a, b)
 
 // waves: 12 (default) or 8 (a tuning alternative, softmax without a position
-// term only).
+// term; the softmax forward with a position term always runs 8).
 hipError_t RBF_CAT(launch_fwd_hr_, RBF_NAME)(const Params& p, int variant, int waves, hipStream_t st) {
   if (!fits(p)) return hipErrorInvalidValue;
   const bool sm = variant == 0;
-  if (p.pos) return sm ? fwd_cfg<true, 12, true>(p, st) : fwd_cfg<false, 12, true>(p, st);
+  // With a position term the softmax forward needs more registers than 12
+  // waves leave (its next Q block and the term's fragments are in flight
+  // together): 8 waves, measured as fast as 12 with spills.
+  if (p.pos) return sm ? fwd_cfg<true, 8, true>(p, st) : fwd_cfg<false, 12, true>(p, st);
   if (waves == 8 && sm) return fwd_cfg<true, 8, false>(p, st);
   return sm ? fwd_cfg<true, 12, false>(p, st) : fwd_cfg<false, 12, false>(p, st);
 }
