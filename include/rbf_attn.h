@@ -126,7 +126,9 @@ int rbf_attn_bwd_stage(const rbf_attn_args* args, void* stream, int stage);
  * the kernels use q + pos and k + pos (each sum rounded to the element type,
  * as two separate elementwise adds of the tensors would store it) wherever
  * the plain entry points use q and k.  pos is a (B, H, N, D) operand like
- * the others (stride_b may be 0: one term shared by the batch).  The
+ * the others: rows (b, h, n) of every b < B, h < H, n < N are read, so a
+ * term shared by the batch (one (H, N, D) tensor) is passed with
+ * stride_b = 0, never with the stride of its own batch-1 shape.  The
  * gradients dq, dk are those of the shifted inputs, which equal the
  * gradients of q, k; the term's own gradient is sum_b (dq + dk) and is left
  * to the caller.  No reference counterpart: it fuses the SuSiE position
