@@ -1,7 +1,7 @@
 """Benchmark of the fused RBF attention hot path on one MI355X.
 
 A step is one forward + backward (3 kernels: fwd, dQ(+Delta), dK/dV) of the
-BASELINE model-shaped configuration (c2_model_bf16: B=32, H=8, N=512+4
+benchmark's model-shaped configuration (c2_model_bf16: B=32, H=8, N=512+4
 registers, D=64, bf16, causal) on synthetic seeded inputs resident in HBM,
 called through the C ABI on torch's current stream.  Prints one JSON line.
 
@@ -145,7 +145,7 @@ def roofline(w, kernel: str, flops: float, seconds: float, peak_tflops: float):
 
 
 def train_step_bench(dev, steps: int, warmup: int):
-    """one next-token training step (bf16 autocast fwd,
+    """Benchmark config 5: one next-token training step (bf16 autocast fwd,
     bwd, AdamW) of the 8-layer d512 RBF transformer on synthetic tokens,
     with the HIP attention kernels.  Returns a dict for the JSON line."""
     import torch

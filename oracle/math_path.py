@@ -1,4 +1,4 @@
-"""The reference's PyTorch math path, restated for the CPU -- TEST / BASELINE
+"""The reference's PyTorch math path, restated for the CPU -- TEST AND CPU-BASELINE
 INFRASTRUCTURE ONLY (used by tests/ and by bench.py's cpu_baseline leg).
 
 softmax:      augmented-dimension SDPA in float32 with autograd backward,

@@ -34,7 +34,7 @@ It restates, in numpy float64, the reference's PyTorch math paths:
 Masking: key j is visible to query i iff (not causal) or j <= i or
 j < num_prefix.  num_prefix = 0 is the reference's is_causal=True mask
 (rbf_attention.py:186-187, 1556-1565); num_prefix = R makes R register tokens
-visible to every query (the BASELINE "registers visible to all").
+visible to every query (the benchmark configurations' "registers visible to all").
 
 How this oracle is pinned (tests/test_oracle.py): the two independent
 restatements (direct distance, augmented SDPA) agree; the augmented one also

@@ -118,7 +118,7 @@ class TransformerBlock(nn.Module):
 
 @dataclasses.dataclass
 class ModelConfig:
-    """Defaults are BASELINE config 5; the reference's defaults are
+    """Defaults are benchmark config 5; the reference's defaults are
     d_model=256, 4 layers, 4 heads, 1 register, pos_weight 0.5, untied logits
     (train_rbf_transformer.py:18-28, rbf_attention.py:1644-1646)."""
 

@@ -62,7 +62,7 @@ class Workload:
         return dataclasses.replace(self, **kw)
 
 
-# The BASELINE configurations (C1..C4); C5 is the model train step.
+# The benchmark configurations (C1..C4); C5 is the model train step.
 C1_TINY = Workload("c1_tiny_fp32", B=2, H=4, content=128, D=64, dtype="fp32")
 C2_MODEL = Workload("c2_model_bf16", B=32, H=8, content=512, D=64, dtype="bf16", key_lognormal=0.5)
 C3_LONG = Workload("c3_long_bf16", B=4, H=16, content=8192, D=128, dtype="bf16", key_lognormal=0.5)

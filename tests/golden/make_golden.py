@@ -3,7 +3,7 @@
 The reference ships no golden vectors (its tests only print), so these
 fixtures are produced by this repository's float64 oracle
 (oracle/rbf_oracle.py, itself pinned by tests/test_oracle.py) on the seeded
-C1 inputs: the first (b, h) slices of BASELINE config 1 (fp32, N = 128
+C1 inputs: the first (b, h) slices of benchmark config 1 (fp32, N = 128
 content + 4 zero register tokens, D = 64, causal).  They freeze the oracle's
 outputs so that a later change to the oracle or to the input generator is
 caught (tests/test_golden.py), and give the GPU tests an input/output pair

@@ -105,7 +105,7 @@ def to_dev(ts, dev):
 
 
 # ---------------------------------------------------------------------------
-# BASELINE configurations
+# Benchmark configurations
 # ---------------------------------------------------------------------------
 def test_c1_tiny_fp32(cuda_device):
     w = wl.C1_TINY
