@@ -1,9 +1,12 @@
 """Benchmark of the fused RBF attention hot path on one MI355X.
 
-A step is one forward + backward (3 kernels: fwd, dQ(+Delta), dK/dV) of the
-benchmark's model-shaped configuration (c2_model_bf16: B=32, H=8, N=512+4
-registers, D=64, bf16, causal) on synthetic seeded inputs resident in HBM,
-called through the C ABI on torch's current stream.  Prints one JSON line.
+A step is one forward + backward of the benchmark's model-shaped
+configuration (c2_model_bf16: B=32, H=8, N=512+4 registers, D=64, bf16,
+causal) on synthetic seeded inputs resident in HBM, called through the C ABI
+(rbf_attn_fwd, rbf_attn_bwd) on torch's current stream.  The backward is one
+kernel where every head fits one work-group (the dQ pass, then the dK/dV
+pass, of each head; c2) and two otherwise (dQ(+Delta), then dK/dV; c3).
+Prints one JSON line.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -106,12 +109,16 @@ def algorithmic_bytes(w, kernel: str) -> float:
     """Compulsory HBM bytes of one launch: every input read once, every
     output written once (element tensors (B,H,N,D), fp32 (B,H,N) vectors).
     fwd: q, k, v -> o (+ L); dQ: q, k, v, dO (+ o, L) -> dq, Delta (or the
-    non-softmax norm offsets); dK/dV: q, k, v, dO, L (+ Delta) -> dk, dv."""
+    non-softmax norm offsets); dK/dV: q, k, v, dO, L (+ Delta) -> dk, dv;
+    bwd (both passes in one kernel): q, k, v, dO (+ o, L) -> dq, dk, dv,
+    Delta (or the norm offsets)."""
     esz = {"bf16": 2, "fp16": 2, "fp32": 4}[w.dtype]
     t = w.B * w.H * w.N * w.D * esz
     vec = 4 * w.B * w.H * w.N
     if kernel == "fwd":
         return 4 * t + (vec if w.softmax else 0)
+    if kernel == "bwd":
+        return (8 * t + 2 * vec) if w.softmax else (7 * t + vec)
     if kernel == "bwd_dq":
         return (6 * t + 3 * vec) if w.softmax else (5 * t + vec)
     return (6 * t + 2 * vec) if w.softmax else (6 * t + vec)
@@ -247,7 +254,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # 300 warmup steps (~25 ms at C2): the first ~100 steps run up to 9 % slower
+    # while the GPU's clocks ramp up.
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", default="c2_model_bf16")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -325,16 +334,23 @@ def main() -> int:
     wall = time.perf_counter() - wall0
     log(f"step: {ms_step * 1e3:.2f} us/step over {args.steps} steps (wall {wall:.3f} s)")
 
-    kern_ms = {"fwd": timed(fwd, args.steps), "bwd_dq": timed(stage(1), args.steps), "bwd_dkdv": timed(stage(2), args.steps)}
+    # Per-kernel averages: each kernel of the step timed in a loop of its own
+    # (events between single launches add their own cost to every launch).
+    # With a one-launch backward, its two stages are timed too, for reference.
+    bwd_launches = _lib.bwd_kernels(a)
+    step_kernels = ("fwd", "bwd") if bwd_launches == 1 else ("fwd", "bwd_dq", "bwd_dkdv")
+    calls = {"fwd": fwd, "bwd": bwd, "bwd_dq": stage(1), "bwd_dkdv": stage(2)}
+    timed_kernels = step_kernels + (("bwd_dq", "bwd_dkdv") if bwd_launches == 1 else ())
+    kern_ms = {kname: timed(calls[kname], args.steps) for kname in timed_kernels}
     for kname, t in kern_ms.items():
-        log(f"  {kname}: {t * 1e3:.2f} us/launch")
+        log(f"  {kname}: {t * 1e3:.2f} us/launch" + ("" if kname in step_kernels else " (stage alone)"))
 
     P = w.visible_pairs() * w.B * w.H
-    per_pair = {"fwd": 4.0, "bwd_dq": 2.0, "bwd_dkdv": 8.0}  # algorithmic flop/pair/D attributed per kernel
+    per_pair = {"fwd": 4.0, "bwd_dq": 2.0, "bwd_dkdv": 8.0, "bwd": 10.0}  # algorithmic flop/pair/D per kernel
     total_flops = w.flops_fwd_bwd()
     tflops = total_flops / (ms_step * 1e-3) / 1e12
     peak = PEAK_TFLOPS[w.dtype]
-    dom = max(kern_ms, key=kern_ms.get)
+    dom = max(step_kernels, key=kern_ms.get)
     dom_flops = per_pair[dom] * w.D * P
 
     result = {
@@ -363,6 +379,7 @@ def main() -> int:
         },
         "pct_of_bf16_peak": round(100.0 * tflops / peak, 3),
         "kernel_us": {kk: round(t * 1e3, 3) for kk, t in kern_ms.items()},
+        "step_kernels": list(step_kernels),
         "roofline": roofline(w, dom, dom_flops, kern_ms[dom] * 1e-3, peak),
     }
     if not args.no_train_step:

@@ -107,7 +107,10 @@ int rbf_attn_fwd(const rbf_attn_args* args, void* stream);
  *                        _rbf_non_softmax_bwd_dq_kernel 1187-1352).
  * Two launches on the stream: the dQ kernel (which also produces Delta, or
  * for the non-softmax variant the per-query norm offsets) and then the
- * dK/dV kernel that consumes them.
+ * dK/dV kernel that consumes them -- or, for heads that fit one work-group's
+ * LDS (bf16/fp16, 32 < D <= 64, N <= 576, at least one head per CU), one
+ * launch that runs both passes of each head back to back
+ * (rbf_attn_bwd_kernels says which).  Same results either way.
  */
 int rbf_attn_bwd(const rbf_attn_args* args, void* stream);
 
@@ -139,6 +142,13 @@ int rbf_attn_bwd_stage(const rbf_attn_args* args, void* stream, int stage);
  */
 int rbf_attn_fwd_pos(const rbf_attn_args* args, const rbf_attn_tensor* pos, void* stream);
 int rbf_attn_bwd_pos(const rbf_attn_args* args, const rbf_attn_tensor* pos, void* stream);
+
+/* Number of kernels rbf_attn_bwd (pos == NULL) or rbf_attn_bwd_pos enqueues
+ * for args: 1 (both passes of a head in one head-resident kernel), 2 (a dQ
+ * kernel, then a dK/dV kernel), 0 for an empty problem, or a negative error
+ * code for invalid args.  Launches nothing.  No reference counterpart: for
+ * callers that time or profile the backward per kernel. */
+int rbf_attn_bwd_kernels(const rbf_attn_args* args, const rbf_attn_tensor* pos);
 
 /* 1 if rbf_attn_fwd_pos / rbf_attn_bwd_pos support args (shape, dtype), 0 if
  * not, or a negative error code for invalid args.  No reference counterpart. */

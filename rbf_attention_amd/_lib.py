@@ -40,6 +40,7 @@ EXPORTS = (
     "rbf_attn_bwd_stage",
     "rbf_attn_fwd_pos",
     "rbf_attn_bwd_pos",
+    "rbf_attn_bwd_kernels",
     "rbf_attn_pos_supported",
     "rbf_attn_decode_workspace_size",
     "rbf_attn_decode",
@@ -154,6 +155,8 @@ def load(path: str | None = None):
         lib.rbf_attn_fwd_pos.restype = ctypes.c_int
         lib.rbf_attn_bwd_pos.argtypes = [ctypes.POINTER(Args), ctypes.POINTER(Tensor), ctypes.c_void_p]
         lib.rbf_attn_bwd_pos.restype = ctypes.c_int
+        lib.rbf_attn_bwd_kernels.argtypes = [ctypes.POINTER(Args), ctypes.POINTER(Tensor)]
+        lib.rbf_attn_bwd_kernels.restype = ctypes.c_int
         lib.rbf_attn_pos_supported.argtypes = [ctypes.POINTER(Args)]
         lib.rbf_attn_pos_supported.restype = ctypes.c_int
         lib.rbf_attn_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs)]
@@ -203,6 +206,15 @@ def pos_supported(args: Args) -> bool:
     if rc < 0:
         raise RbfAttnError(rc, load().rbf_attn_last_error().decode(errors="replace"))
     return rc == 1
+
+
+def bwd_kernels(args: Args, pos: Tensor | None = None) -> int:
+    """Kernels rbf_attn_bwd (or rbf_attn_bwd_pos with pos) enqueues for args."""
+    lib = load()
+    rc = lib.rbf_attn_bwd_kernels(ctypes.byref(args), ctypes.byref(pos) if pos is not None else None)
+    if rc < 0:
+        raise RbfAttnError(rc, lib.rbf_attn_last_error().decode(errors="replace"))
+    return rc
 
 
 def call_pos(fn_name: str, args, pos: Tensor, stream: int) -> None:

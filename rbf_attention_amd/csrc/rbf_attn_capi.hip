@@ -314,7 +314,15 @@ static int bwd_impl(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* st
   if (pos && (rc = set_pos(a, pos, p))) return rc;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
-  if (stage == 0 || stage == 1) {
+  if (stage == 0) {
+    switch (a->dtype) {
+      case RBF_ATTN_BF16: e = rbf::launch_bwd_bf16(p, a->variant, st); break;
+      case RBF_ATTN_FP16: e = rbf::launch_bwd_fp16(p, a->variant, st); break;
+      default: e = rbf::launch_bwd_fp32(p, a->variant, st); break;
+    }
+    return launched(e, "backward");
+  }
+  if (stage == 1) {
     switch (a->dtype) {
       case RBF_ATTN_BF16: e = rbf::launch_bwd_dq_bf16(p, a->variant, st); break;
       case RBF_ATTN_FP16: e = rbf::launch_bwd_dq_fp16(p, a->variant, st); break;
@@ -322,7 +330,7 @@ static int bwd_impl(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* st
     }
     if ((rc = launched(e, "backward dQ"))) return rc;
   }
-  if (stage == 0 || stage == 2) {
+  if (stage == 2) {
     switch (a->dtype) {
       case RBF_ATTN_BF16: e = rbf::launch_bwd_dkdv_bf16(p, a->variant, st); break;
       case RBF_ATTN_FP16: e = rbf::launch_bwd_dkdv_fp16(p, a->variant, st); break;
@@ -341,6 +349,19 @@ int rbf_attn_bwd_pos(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* s
     return fail(RBF_ATTN_EINVAL_PTR, "pos: null descriptor");
   }
   return bwd_impl(a, pos, stream, 0);
+}
+
+int rbf_attn_bwd_kernels(const rbf_attn_args* a, const rbf_attn_tensor* pos) {
+  int rc = check_common(a);
+  if (rc) return rc;
+  if ((long long)a->B * a->H * a->N == 0) return 0;
+  rbf::Params p = make_params(a);
+  if (pos && (rc = set_pos(a, pos, p))) return rc;
+  switch (a->dtype) {
+    case RBF_ATTN_BF16: return rbf::bwd_kernels_bf16(p);
+    case RBF_ATTN_FP16: return rbf::bwd_kernels_fp16(p);
+    default: return rbf::bwd_kernels_fp32(p);
+  }
 }
 
 int rbf_attn_bwd_stage(const rbf_attn_args* a, void* stream, int stage) {

@@ -50,37 +50,55 @@ __device__ inline void hr_unit(int u, int& row, int& ch) {
 // stored.  The code is branch-free: with conditional stores here the compiler's
 // wait-count insertion no longer tells later LDS reads of other tiles apart
 // from outstanding LDS-DMA loads, and makes them wait for those loads.
+// Two tiles in flight: fetch() issues the global loads into registers, put()
+// stores them (with the position term added to the first) into chunk-major
+// LDS tiles.  Between the two the loads stay outstanding, so a caller can
+// wait at a barrier meanwhile.
+template <typename T, int ROWS, int DP, int NT, bool ADD>
+struct HrTiles2 {
+  typedef typename Elem<T>::frag frag;
+  static constexpr int PB = (ROWS * (DP / 8) + NT - 1) / NT;
+  frag ra[PB], rb[PB], rp[ADD ? PB : 1];
+
+  __device__ inline void fetch(const T* A, int64_t sa, const T* B, int64_t sb, int rows, int org, int N, int D, int tid,
+                               const T* addA, int64_t asa) {
+    const int units = rows * (DP / 8);
+#pragma unroll
+    for (int j = 0; j < PB; ++j) {
+      const int u = tid + j * NT;
+      int row, ch;
+      hr_unit<DP>(u, row, ch);
+      const int tok = org + row;
+      const bool ok = u < units && tok >= 0 && tok < N && ch * 8 < D;
+      ra[j] = ok ? ld8<T>(A + (int64_t)tok * sa + ch * 8) : zero_frag<T>();
+      rb[j] = ok ? ld8<T>(B + (int64_t)tok * sb + ch * 8) : zero_frag<T>();
+      if constexpr (ADD) rp[j] = ok ? ld8<T>(addA + (int64_t)tok * asa + ch * 8) : zero_frag<T>();
+    }
+  }
+
+  __device__ inline void put(T* sA, T* sB, int tid) {
+    typedef CLayout<ROWS> L;
+    add_pos<T, ADD>(ra, rp, PB);
+    // Units past the tile store into the padding after chunk column 0
+    // instead of branching around the store.
+#pragma unroll
+    for (int j = 0; j < PB; ++j) {
+      const int u = tid + j * NT;
+      int row, ch;
+      hr_unit<DP>(u, row, ch);
+      const int o = u < ROWS * (DP / 8) ? L::off(row, 8 * ch) : L::off(ROWS, 0);
+      st8<T>(sA + o, ra[j]);
+      st8<T>(sB + o, rb[j]);
+    }
+  }
+};
+
 template <typename T, int ROWS, int DP, int NT, bool ADD>
 __device__ inline void hr_load2(const T* A, int64_t sa, T* sA, const T* B, int64_t sb, T* sB, int rows, int org,
                                 int N, int D, int tid, const T* addA, int64_t asa) {
-  typedef typename Elem<T>::frag frag;
-  typedef CLayout<ROWS> L;
-  constexpr int PB = (ROWS * (DP / 8) + NT - 1) / NT;
-  const int units = rows * (DP / 8);
-  frag ra[PB], rb[PB], rp[ADD ? PB : 1];
-#pragma unroll
-  for (int j = 0; j < PB; ++j) {
-    const int u = tid + j * NT;
-    int row, ch;
-    hr_unit<DP>(u, row, ch);
-    const int tok = org + row;
-    const bool ok = u < units && tok >= 0 && tok < N && ch * 8 < D;
-    ra[j] = ok ? ld8<T>(A + (int64_t)tok * sa + ch * 8) : zero_frag<T>();
-    rb[j] = ok ? ld8<T>(B + (int64_t)tok * sb + ch * 8) : zero_frag<T>();
-    if constexpr (ADD) rp[j] = ok ? ld8<T>(addA + (int64_t)tok * asa + ch * 8) : zero_frag<T>();
-  }
-  add_pos<T, ADD>(ra, rp, PB);
-  // Units past the tile store into the padding after chunk column 0 instead
-  // of branching around the store.
-#pragma unroll
-  for (int j = 0; j < PB; ++j) {
-    const int u = tid + j * NT;
-    int row, ch;
-    hr_unit<DP>(u, row, ch);
-    const int o = u < ROWS * (DP / 8) ? L::off(row, 8 * ch) : L::off(ROWS, 0);
-    st8<T>(sA + o, ra[j]);
-    st8<T>(sB + o, rb[j]);
-  }
+  HrTiles2<T, ROWS, DP, NT, ADD> t;
+  t.fetch(A, sa, B, sb, rows, org, N, D, tid, addA, asa);
+  t.put(sA, sB, tid);
 }
 
 // nrm[row] = -0.5 ||row||^2 of a resident chunk-major tile (fp32, from the
@@ -392,17 +410,17 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
 //   -Delta), dS = P dP, dV^T += dO^T P, dK^T += Q^T dS, colsum += dS,
 // with K and V in registers and no barrier after the load.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int NB, bool SOFTMAX, bool POS = false>
-__global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p) {
+// XFER: runs after a dQ pass of the same head in the same LDS.  That pass
+// left the per-query term it forms (softmax: sDel = -Delta; non-softmax:
+// sOff = -off / c) in LDS, so it is neither read from global memory nor
+// staged here, and the tiles are stored only after a barrier.
+template <typename T, int DP, int W, int NB, bool SOFTMAX, bool POS, bool XFER = false>
+__device__ __forceinline__ void bwd_dkdv_hr_body(const Params& p, T* sQ, T* sD, float* sOff, float* sDel) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   static_assert(sizeof(T) == 2, "head-resident tiles are chunk-major 16-bit tiles");
   constexpr int ROWS = 32 * NB, NT = 64 * W, KS = DP / 16, ND = DP / 32;
   typedef CLayout<ROWS> L;
-  __shared__ __attribute__((aligned(16))) T sQ[L::template size<DP>()];
-  __shared__ __attribute__((aligned(16))) T sD[L::template size<DP>()];
-  __shared__ __attribute__((aligned(16))) float sOff[ROWS];
-  __shared__ __attribute__((aligned(16))) float sDel[ROWS];
 
   if (p.nblk > NB) return;  // the host launches this kernel only for heads that fit
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
@@ -448,17 +466,24 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
   for (int j = 0; j < RPT; ++j) {
     const int r = tid + j * NT, tok = org + r;
     const bool ok = r < 32 * nblk && tok >= 0 && tok < N;
-    offv[j] = ok ? offg[tok] : 0.f;
-    delv[j] = (SOFTMAX && ok) ? delg[tok] : 0.f;
+    offv[j] = (ok && !(XFER && !SOFTMAX)) ? offg[tok] : 0.f;
+    delv[j] = (SOFTMAX && !XFER && ok) ? delg[tok] : 0.f;
   }
-  hr_load2<T, ROWS, DP, NT, POS>(Q, p.sq[2], sQ, dO, p.sdo[2], sD, 32 * nblk, org, N, D, tid, Pos, p.spos[2]);
+  {
+    HrTiles2<T, ROWS, DP, NT, POS> tiles;
+    tiles.fetch(Q, p.sq[2], dO, p.sdo[2], 32 * nblk, org, N, D, tid, Pos, p.spos[2]);
+    // After a dQ pass in the same LDS: wait until every wave is done with its
+    // tiles (the loads above stay in flight meanwhile).
+    if constexpr (XFER) __syncthreads();
+    tiles.put(sQ, sD, tid);
+  }
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int r = tid + j * NT, tok = org + r;
     const bool ok = tok >= 0 && tok < N;
     if (r < 32 * nblk) {
-      sOff[r] = ok ? -offv[j] * inv_c : -__builtin_inff();  // padding queries: P = 0
-      sDel[r] = ok ? -delv[j] : 0.f;
+      if (!(XFER && !SOFTMAX)) sOff[r] = ok ? -offv[j] * inv_c : -__builtin_inff();  // padding queries: P = 0
+      if (!(XFER && SOFTMAX)) sDel[r] = ok ? -delv[j] : 0.f;
     }
   }
   __syncthreads();
@@ -574,16 +599,16 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p)
 // with the next key block's K and V rows read one block ahead and no
 // barrier after the load.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int NB, bool SOFTMAX, bool POS = false>
-__global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
+// sX (optional): the per-query term the dK/dV pass needs is also stored there,
+// in that pass's LDS form (softmax: -Delta; non-softmax: -off / c, -inf for
+// padding queries).
+template <typename T, int DP, int W, int NB, bool SOFTMAX, bool POS>
+__device__ __forceinline__ void bwd_dq_hr_body(const Params& p, T* sK, T* sV, float* sKn, float* sX = nullptr) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   static_assert(sizeof(T) == 2, "head-resident tiles are chunk-major 16-bit tiles");
   constexpr int ROWS = 32 * NB, NT = 64 * W, KS = DP / 16, ND = DP / 32;
   typedef CLayout<ROWS> L;
-  __shared__ __attribute__((aligned(16))) T sK[L::template size<DP>()];
-  __shared__ __attribute__((aligned(16))) T sV[L::template size<DP>()];
-  __shared__ __attribute__((aligned(16))) float sKn[ROWS];
 
   if (p.nblk > NB) return;  // the host launches this kernel only for heads that fit
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
@@ -650,6 +675,8 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
       off = c * 0.5f * xhalf_sum(ss);
       if (qvalid && h == 0) p.lse[(int64_t)bh * N + qtok] = off;
     }
+    if (sX != nullptr && h == 0)
+      sX[32 * qb + n] = SOFTMAX ? -dlt : (qvalid ? -off * (1.f / c) : -__builtin_inff());
     const f32x16_t ndel = splat16(-dlt);
     // key blocks [0, kend) hold every key some query of the block sees
     const int kend = causal ? min(nblk, ((max(q0 + 31, npre - 1) - org) >> 5) + 1) : nblk;
@@ -726,6 +753,50 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
         }
     }
   }
+}
+
+template <typename T, int DP, int W, int NB, bool SOFTMAX, bool POS = false>
+__global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_hr_kernel(const Params p) {
+  typedef CLayout<32 * NB> L;
+  __shared__ __attribute__((aligned(16))) T sQ[L::template size<DP>()];
+  __shared__ __attribute__((aligned(16))) T sD[L::template size<DP>()];
+  __shared__ __attribute__((aligned(16))) float sOff[32 * NB];
+  __shared__ __attribute__((aligned(16))) float sDel[32 * NB];
+  bwd_dkdv_hr_body<T, DP, W, NB, SOFTMAX, POS>(p, sQ, sD, sOff, sDel);
+}
+
+template <typename T, int DP, int W, int NB, bool SOFTMAX, bool POS = false>
+__global__ __launch_bounds__(64 * W) void rbf_bwd_dq_hr_kernel(const Params p) {
+  typedef CLayout<32 * NB> L;
+  __shared__ __attribute__((aligned(16))) T sK[L::template size<DP>()];
+  __shared__ __attribute__((aligned(16))) T sV[L::template size<DP>()];
+  __shared__ __attribute__((aligned(16))) float sKn[32 * NB];
+  bwd_dq_hr_body<T, DP, W, NB, SOFTMAX, POS>(p, sK, sV, sKn);
+}
+
+// ---------------------------------------------------------------------------
+// The whole backward of a head in one launch: the dQ pass (K, V resident;
+// writes Delta) then, after a barrier, the dK/dV pass (Q, dO resident; reads
+// that Delta) in the same LDS.  One kernel boundary fewer than two launches,
+// and a CU that finishes its dQ pass starts its dK/dV load while others still
+// compute.
+// ---------------------------------------------------------------------------
+template <typename T, int DP, int W, int NB, bool SOFTMAX, bool POS = false>
+__global__ __launch_bounds__(64 * W) void rbf_bwd_hr_kernel(const Params p) {
+  typedef CLayout<32 * NB> L;
+  __shared__ __attribute__((aligned(16))) T sA[L::template size<DP>()];
+  __shared__ __attribute__((aligned(16))) T sB[L::template size<DP>()];
+  __shared__ __attribute__((aligned(16))) float s1[32 * NB];
+  __shared__ __attribute__((aligned(16))) float s2[32 * NB];
+  // The per-query term passes from one pass to the other through s2 (the
+  // global copy is written too, as the two-launch form writes it, but not
+  // read back).  The dK/dV pass requests its first loads before the barrier
+  // that ends the dQ pass.
+  bwd_dq_hr_body<T, DP, W, NB, SOFTMAX, POS>(p, sA, sB, s1, s2);
+  if constexpr (SOFTMAX)
+    bwd_dkdv_hr_body<T, DP, W, NB, SOFTMAX, POS, true>(p, sA, sB, s1, s2);
+  else
+    bwd_dkdv_hr_body<T, DP, W, NB, SOFTMAX, POS, true>(p, sA, sB, s2, s1);
 }
 
 }  // namespace rbf

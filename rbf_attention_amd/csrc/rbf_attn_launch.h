@@ -10,10 +10,14 @@ struct Params;
 struct DecodeParams;
 
 // variant: 0 = softmax, 1 = non-softmax.  Return the launch status.
+// launch_bwd_* is the whole backward (dQ, then dK/dV); bwd_kernels_* is the
+// number of kernels it enqueues for p (1 or 2).
 #define RBF_DECLARE_LAUNCHERS(NAME)                                              \
   hipError_t launch_fwd_##NAME(const Params& p, int variant, hipStream_t st);   \
   hipError_t launch_bwd_dq_##NAME(const Params& p, int variant, hipStream_t st); \
   hipError_t launch_bwd_dkdv_##NAME(const Params& p, int variant, hipStream_t st); \
+  hipError_t launch_bwd_##NAME(const Params& p, int variant, hipStream_t st);      \
+  int bwd_kernels_##NAME(const Params& p);                                          \
   hipError_t launch_decode_##NAME(const DecodeParams& p, int variant, hipStream_t st);
 
 RBF_DECLARE_LAUNCHERS(bf16)
@@ -30,7 +34,8 @@ constexpr int kHrMaxBlocks = 18;
 #define RBF_DECLARE_HR_LAUNCHERS(NAME)                                                         \
   hipError_t launch_fwd_hr_##NAME(const Params& p, int variant, int waves, hipStream_t st);   \
   hipError_t launch_bwd_dq_hr_##NAME(const Params& p, int variant, hipStream_t st);           \
-  hipError_t launch_bwd_dkdv_hr_##NAME(const Params& p, int variant, hipStream_t st);
+  hipError_t launch_bwd_dkdv_hr_##NAME(const Params& p, int variant, hipStream_t st);     \
+  hipError_t launch_bwd_hr_##NAME(const Params& p, int variant, hipStream_t st);
 
 RBF_DECLARE_HR_LAUNCHERS(bf16)
 RBF_DECLARE_HR_LAUNCHERS(fp16)

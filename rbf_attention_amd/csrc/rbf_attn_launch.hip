@@ -126,6 +126,16 @@ hipError_t hr_dkdv(const Params& p, bool sm, hipStream_t st) {
 #endif
 }
 
+hipError_t hr_bwd(const Params& p, bool sm, hipStream_t st) {
+#if RBF_ELEM_ID == 0
+  return launch_bwd_hr_bf16(p, sm ? 0 : 1, st);
+#elif RBF_ELEM_ID == 1
+  return launch_bwd_hr_fp16(p, sm ? 0 : 1, st);
+#else
+  return hipErrorInvalidValue;
+#endif
+}
+
 // Head-resident kernels (16-bit): the head's nblk blocks fit the kernel's LDS
 // tiles (nb_max blocks) and there are at least as many heads as CUs, so one
 // work-group per head fills the GPU.  RBF_ATTN_HR=0 disables them, =1 uses
@@ -368,6 +378,28 @@ hipError_t dkdv_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH
 
 #undef RBF_DISPATCH
 
+// Whole backward.  Where both backward kernels take the head-resident form,
+// one launch runs a head's dQ pass and then its dK/dV pass
+// (rbf_bwd_hr_kernel): one kernel boundary fewer, and the dK/dV pass's loads
+// overlap the end of the dQ pass (C2: 85 against 89.6 us per step).
+// RBF_ATTN_BWD_MERGED=0 keeps the two launches.
+bool bwd_one_launch(const Params& p) {
+  if constexpr (kIsF32) {
+    return false;
+  } else {
+    static const int merged = env_choice("RBF_ATTN_BWD_MERGED");
+    if (merged == 0 || p.D <= 32 || p.D > 64) return false;
+    return p.pos ? p.nblk <= kHrBlocks64 : use_hr(p, kHrBlocks64, 2) && use_hr(p, kHrBlocks64, 4);
+  }
+}
+
+hipError_t bwd_any(const Params& p, int variant, hipStream_t st) {
+  if (bwd_one_launch(p)) return hr_bwd(p, variant == 0, st);
+  hipError_t e = dq_any(p, variant, st);
+  if (e != hipSuccess) return e;
+  return dkdv_any(p, variant, st);
+}
+
 template <int DP, bool SM>
 hipError_t decode_dp(const DecodeParams& p, hipStream_t st) {
   constexpr int W = kIsF32 ? 2 : 4;
@@ -407,6 +439,10 @@ hipError_t RBF_CAT(launch_bwd_dq_, RBF_NAME)(const Params& p, int variant, hipSt
 hipError_t RBF_CAT(launch_bwd_dkdv_, RBF_NAME)(const Params& p, int variant, hipStream_t st) {
   return dkdv_any(p, variant, st);
 }
+hipError_t RBF_CAT(launch_bwd_, RBF_NAME)(const Params& p, int variant, hipStream_t st) {
+  return bwd_any(p, variant, st);
+}
+int RBF_CAT(bwd_kernels_, RBF_NAME)(const Params& p) { return bwd_one_launch(p) ? 1 : 2; }
 hipError_t RBF_CAT(launch_decode_, RBF_NAME)(const DecodeParams& p, int variant, hipStream_t st) {
   return decode_any(p, variant, st);
 }

@@ -45,6 +45,12 @@ hipError_t dkdv_cfg(const Params& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <bool SM, bool POS>
+hipError_t bwd_cfg(const Params& p, hipStream_t st) {
+  hipLaunchKernelGGL((rbf_bwd_hr_kernel<Elt, DP, 8, NB, SM, POS>), dim3(heads(p)), dim3(64 * 8), 0, st, p);
+  return hipGetLastError();
+}
+
 bool fits(const Params& p) { return p.D > 32 && p.D <= DP && p.nblk <= NB; }
 
 }  // namespace
@@ -82,6 +88,14 @@ hipError_t RBF_CAT(launch_bwd_dkdv_hr_, RBF_NAME)(const Params& p, int variant, 
   const bool sm = variant == 0;
   if (p.pos) return sm ? dkdv_cfg<true, true>(p, st) : dkdv_cfg<false, true>(p, st);
   return sm ? dkdv_cfg<true, false>(p, st) : dkdv_cfg<false, false>(p, st);
+}
+
+// dQ then dK/dV of each head in one launch (rbf_bwd_hr_kernel).
+hipError_t RBF_CAT(launch_bwd_hr_, RBF_NAME)(const Params& p, int variant, hipStream_t st) {
+  if (!fits(p)) return hipErrorInvalidValue;
+  const bool sm = variant == 0;
+  if (p.pos) return sm ? bwd_cfg<true, true>(p, st) : bwd_cfg<false, true>(p, st);
+  return sm ? bwd_cfg<true, false>(p, st) : bwd_cfg<false, false>(p, st);
 }
 
 }  // namespace rbf

@@ -20,6 +20,8 @@ def test_algorithmic_bytes_c2():
     assert bench.algorithmic_bytes(w, "fwd") == 4 * t + v
     assert bench.algorithmic_bytes(w, "bwd_dq") == 6 * t + 3 * v
     assert bench.algorithmic_bytes(w, "bwd_dkdv") == 6 * t + 2 * v
+    # one-launch backward: q, k, v, dO, o, L in; dq, dk, dv, Delta out
+    assert bench.algorithmic_bytes(w, "bwd") == 8 * t + 2 * v
 
 
 def test_algorithmic_bytes_non_softmax():
@@ -29,6 +31,7 @@ def test_algorithmic_bytes_non_softmax():
     assert bench.algorithmic_bytes(w, "fwd") == 4 * t
     assert bench.algorithmic_bytes(w, "bwd_dq") == 5 * t + v
     assert bench.algorithmic_bytes(w, "bwd_dkdv") == 6 * t + v
+    assert bench.algorithmic_bytes(w, "bwd") == 7 * t + v
 
 
 def test_roofline_bound_follows_intensity():

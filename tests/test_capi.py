@@ -154,6 +154,22 @@ def test_pos_entry_points_reject_before_launch(lib):
         assert fn(ctypes.byref(good_args(N=0)), ctypes.byref(pos), None) == 0
 
 
+def test_bwd_kernels_query(lib):
+    """Shapes decided without a device query: fp32 and D > 64 always take two
+    launches, a fused position term on a head that fits takes one."""
+    pos = _lib.Tensor(FAKE + 0x3000000, 0, 64 * 64, 64)
+
+    def n(over, p=None):
+        return lib.rbf_attn_bwd_kernels(ctypes.byref(good_args(**over)), ctypes.byref(p) if p else None)
+
+    assert n(dict(dtype=2)) == 2 and n(dict(D=128)) == 2 and n(dict(D=32)) == 2
+    assert n(dict(N=516), pos) == 1 and n(dict(N=516, dtype=1), pos) == 1
+    assert n(dict(N=577), pos) == -8 and n(dict(D=128), pos) == -8
+    assert n(dict(N=0)) == 0
+    assert n(dict(dtype=7)) == -2 and n(dict(D=60)) == -4
+    assert lib.rbf_attn_bwd_kernels(None, None) == -1
+
+
 # ---------------------------------------------------------------------------
 # decode entry points
 # ---------------------------------------------------------------------------

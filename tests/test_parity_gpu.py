@@ -311,6 +311,44 @@ def test_strided_views_like_the_model(cuda_device):
     compare_case(q, k, v, do, tag="strided")
 
 
+@pytest.mark.parametrize("softmax", [True, False])
+def test_one_launch_backward_equals_two_stages(cuda_device, softmax):
+    """At B*H = 256 heads of N <= 576 the backward is one launch (both passes
+    of a head in one work-group, the per-query term passed through LDS); it
+    must give the two-launch form's dQ, dK, dV and workspace bit for bit."""
+    from rbf_attention_amd import _lib
+
+    B, H, N, D, dtype = 16, 16, 516, 64, torch.bfloat16
+    q, k, v, do = rand_inputs(B, H, N, D, dtype, cuda_device, std=1.0 if softmax else 0.5, seed=33)
+    bufs = {"q": q, "k": k, "v": v, "dout": do}
+    for f in ("o", "dq", "dk", "dv"):
+        bufs[f] = torch.zeros_like(q)
+    bufs["lse"] = torch.zeros((B, H, N), device=cuda_device, dtype=torch.float32)
+    bufs["delta"] = torch.zeros_like(bufs["lse"])
+    a = _lib.Args()
+    a.abi_version, a.variant, a.dtype = _lib.ABI_VERSION, 0 if softmax else 1, _lib.DTYPE_CODES[dtype]
+    a.B, a.H, a.N, a.D, a.causal, a.num_prefix, a.gamma = B, H, N, D, 1, 4, 1.0 / (2 * math.sqrt(D))
+    for f in ("q", "k", "v", "o", "dout", "dq", "dk", "dv"):
+        setattr(a, f, _lib.tensor_desc(bufs[f]))
+    a.lse, a.delta = bufs["lse"].data_ptr(), bufs["delta"].data_ptr()
+    assert _lib.bwd_kernels(a) == 1
+    sp = torch.cuda.current_stream(cuda_device).cuda_stream
+    _lib.call("rbf_attn_fwd", a, sp)
+    keep = ("dq", "dk", "dv", "lse", "delta")
+    _lib.call("rbf_attn_bwd", a, sp)
+    one = {f: bufs[f].clone() for f in keep}
+    for f in ("dq", "dk", "dv", "delta"):
+        bufs[f].zero_()
+    if not softmax:
+        bufs["lse"].zero_()  # the non-softmax backward's norm-offset workspace
+    _lib.call("rbf_attn_bwd_stage", a, sp, 1)
+    _lib.call("rbf_attn_bwd_stage", a, sp, 2)
+    torch.cuda.synchronize()
+    for f in keep:
+        assert torch.equal(one[f], bufs[f]), f"{f}: max diff {(one[f].float() - bufs[f].float()).abs().max().item():.3e}"
+    assert one["dq"].abs().sum() > 0 and one["dk"].abs().sum() > 0
+
+
 def test_deterministic(cuda_device):
     q, k, v, do = rand_inputs(2, 4, 300, 64, torch.bfloat16, cuda_device, seed=21)
     a = run_ours(q, k, v, do, True, True, None, 0)
