@@ -334,6 +334,26 @@ def main() -> int:
     wall = time.perf_counter() - wall0
     log(f"step: {ms_step * 1e3:.2f} us/step over {args.steps} steps (wall {wall:.3f} s)")
 
+    # The same step captured once in a HIP graph and replayed K times (no
+    # host launch cost per kernel); reported beside `value`, not as it.  On
+    # MI355X the replay measured slower than eager launches (C2 90 against
+    # 80 us), so the eager step is the one reported.
+    def cur_step():
+        s = torch.cuda.current_stream(dev).cuda_stream
+        _lib.call("rbf_attn_fwd", a, s)
+        _lib.call("rbf_attn_bwd", a, s)
+
+    ms_graph = None
+    try:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            cur_step()
+        graph.replay()
+        ms_graph = timed(graph.replay, args.steps)
+        log(f"graph step: {ms_graph * 1e3:.2f} us/step")
+    except RuntimeError as e:  # reported as null; the eager measurement stands
+        log(f"graph step: capture failed ({e})")
+
     # Per-kernel averages: each kernel of the step timed in a loop of its own
     # (events between single launches add their own cost to every launch).
     # With a one-launch backward, its two stages are timed too, for reference.
@@ -378,6 +398,7 @@ def main() -> int:
             "flops_per_step": total_flops,
         },
         "pct_of_bf16_peak": round(100.0 * tflops / peak, 3),
+        "graph_step_us": round(ms_graph * 1e3, 3) if ms_graph is not None else None,
         "kernel_us": {kk: round(t * 1e3, 3) for kk, t in kern_ms.items()},
         "step_kernels": list(step_kernels),
         "roofline": roofline(w, dom, dom_flops, kern_ms[dom] * 1e-3, peak),
