@@ -31,6 +31,7 @@ import torch
 
 import rbf_attention_amd as ra
 from oracle import rbf_oracle as ro
+from rbf_attention_amd import _lib
 from rbf_attention_amd import workloads as wl
 
 pytestmark = pytest.mark.gpu
@@ -234,6 +235,9 @@ def test_queries_far_from_every_key(cuda_device, dtype, shift):
         (300, 64, torch.float16, True, True, 0, 0.0),
         (200, 40, torch.bfloat16, True, True, 0, 0.0),
         (300, 64, torch.bfloat16, True, True, 0, 6.0),
+        (576, 64, torch.bfloat16, True, True, 0, 0.0),  # 18 blocks: the largest head that fits LDS
+        (576, 64, torch.bfloat16, False, True, 0, 0.0),
+        (577, 64, torch.bfloat16, True, True, 0, 0.0),  # one token more: the streaming kernels
     ],
 )
 def test_head_resident_shapes(cuda_device, N, D, dtype, softmax, causal, num_prefix, shift):
@@ -243,6 +247,12 @@ def test_head_resident_shapes(cuda_device, N, D, dtype, softmax, causal, num_pre
     queries far from every key (the forward's per-block rerun with an online
     max).  Compared on a 2 x 2 corner of (b, h) slices."""
     q, k, v, do = rand_inputs(16, 16, N, D, dtype, cuda_device, std=1.0 if softmax else 0.5, seed=N + D)
+    a = _lib.Args()
+    a.abi_version, a.variant, a.dtype = _lib.ABI_VERSION, 0 if softmax else 1, _lib.DTYPE_CODES[dtype]
+    a.B, a.H, a.N, a.D, a.causal, a.gamma = 16, 16, N, D, int(causal), 0.1
+    for f in ("q", "k", "v", "o", "dout", "dq", "dk", "dv"):
+        setattr(a, f, _lib.tensor_desc(q))
+    assert _lib.bwd_kernels(a) == (1 if N <= 576 else 2)
     if shift:
         q = q.clone()
         q[:2, ::2, :90] += shift
@@ -316,8 +326,6 @@ def test_one_launch_backward_equals_two_stages(cuda_device, softmax):
     """At B*H = 256 heads of N <= 576 the backward is one launch (both passes
     of a head in one work-group, the per-query term passed through LDS); it
     must give the two-launch form's dQ, dK, dV and workspace bit for bit."""
-    from rbf_attention_amd import _lib
-
     B, H, N, D, dtype = 16, 16, 516, 64, torch.bfloat16
     q, k, v, do = rand_inputs(B, H, N, D, dtype, cuda_device, std=1.0 if softmax else 0.5, seed=33)
     bufs = {"q": q, "k": k, "v": v, "dout": do}
