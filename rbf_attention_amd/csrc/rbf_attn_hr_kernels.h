@@ -677,7 +677,7 @@ __device__ __forceinline__ void bwd_dq_hr_body(const Params& p, T* sK, T* sV, fl
     }
     if (sX != nullptr && h == 0)
       sX[32 * qb + n] = SOFTMAX ? -dlt : (qvalid ? -off * (1.f / c) : -__builtin_inff());
-    const f32x16_t ndel = splat16(-dlt);
+    const f32x16_t ndel = SOFTMAX ? splat16(-dlt) : zero16();  // +0: the MFMA's inline constant
     // key blocks [0, kend) hold every key some query of the block sees
     const int kend = causal ? min(nblk, ((max(q0 + 31, npre - 1) - org) >> 5) + 1) : nblk;
 

@@ -654,8 +654,11 @@ __device__ inline int first_query(int j, bool causal, int npre) {
 }
 
 // Keys along the accumulator rows (fwd, dQ: lane = query): element i holds key
-// k0 + crow(i, h); keep it iff 0 <= key <= jmax.
+// k0 + crow(i, h); keep it iff 0 <= key <= jmax.  Callers apply the masks
+// only to the blocks that need one; the empty volatile asm keeps the compiler
+// from turning that branch into compares and selects run on every block.
 __device__ inline void mask_key_rows(f32x16_t& s, int k0, int h, int jmax) {
+  asm volatile("");
   const int lo = -k0 - 4 * h, hi = jmax - k0 - 4 * h;
 #pragma unroll
   for (int i = 0; i < 16; ++i)
@@ -664,6 +667,7 @@ __device__ inline void mask_key_rows(f32x16_t& s, int k0, int h, int jmax) {
 // Queries along the accumulator rows (dK/dV: lane = key): element i holds
 // query q0 + crow(i, h); keep it iff query >= ilo (queries never exceed N-1).
 __device__ inline void mask_query_rows(f32x16_t& s, int q0, int h, int ilo) {
+  asm volatile("");
   const int lo = ilo - q0 - 4 * h;
 #pragma unroll
   for (int i = 0; i < 16; ++i)
@@ -986,7 +990,7 @@ __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int gr
       off[j] = c * 0.5f * s;
       if (qvalid && h == 0) p.lse[(int64_t)bh * N + qtok[j]] = off[j];
     }
-    ndel[j] = splat16(-dlt);
+    ndel[j] = SOFTMAX ? splat16(-dlt) : zero16();  // +0: the MFMA's inline constant, no copies
   }
 
   f32x16_t dqacc[QPW][ND];
