@@ -42,18 +42,13 @@ __device__ inline void hr_unit(int u, int& row, int& ch) {
   row = 4 * (rest / CG) + ((u >> 2) & 3);
 }
 
-// Loads rows [0, rows) -- tokens org + row -- of two (N, D) slices into
-// chunk-major LDS tiles of ROWS rows; tokens outside [0, N) and features
-// >= D are zero; when ADD, addA (row stride asa) is added to every row of the
-// first slice (position term).  Every chunk of a thread is requested
-// before the first is
-// stored.  The code is branch-free: with conditional stores here the compiler's
-// wait-count insertion no longer tells later LDS reads of other tiles apart
-// from outstanding LDS-DMA loads, and makes them wait for those loads.
-// Two tiles in flight: fetch() issues the global loads into registers, put()
-// stores them (with the position term added to the first) into chunk-major
-// LDS tiles.  Between the two the loads stay outstanding, so a caller can
-// wait at a barrier meanwhile.
+// Two head tiles in flight: fetch() requests rows [0, rows) -- tokens
+// org + row -- of two (N, D) slices into registers (tokens outside [0, N) and
+// features >= D read as zero; when ADD, the rows of addA, row stride asa, too),
+// put() stores them into chunk-major LDS tiles of ROWS rows, the position term
+// added to the first slice.  Every chunk of a thread is requested before the
+// first is stored, and between the two calls the loads stay outstanding, so a
+// caller can wait at a barrier meanwhile.
 template <typename T, int ROWS, int DP, int NT, bool ADD>
 struct HrTiles2 {
   typedef typename Elem<T>::frag frag;
@@ -93,6 +88,7 @@ struct HrTiles2 {
   }
 };
 
+// fetch() then put(): both tiles of a head loaded into LDS.
 template <typename T, int ROWS, int DP, int NT, bool ADD>
 __device__ inline void hr_load2(const T* A, int64_t sa, T* sA, const T* B, int64_t sb, T* sB, int rows, int org,
                                 int N, int D, int tid, const T* addA, int64_t asa) {
