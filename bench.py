@@ -5,15 +5,30 @@ configuration (c2_model_bf16: B=32, H=8, N=512+4 registers, D=64, bf16,
 causal) on synthetic seeded inputs resident in HBM, called through the C ABI
 (rbf_attn_fwd, rbf_attn_bwd) on torch's current stream.  The backward is one
 kernel where every head fits one work-group (the dQ pass, then the dK/dV
-pass, of each head; c2) and two otherwise (dQ(+Delta), then dK/dV; c3).
+pass, of each head; c2) and two otherwise (dQ(+Delta), then dK/dV; c3, c4).
 Prints one JSON line.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--quick]
+
+Timing protocol
+  * Before the W warmup steps the step runs for --ramp-seconds (default 0.4 s)
+    untimed, so that the timed steps see the GPU's steady clocks: in a fresh
+    process the first ~100 C2 steps ran up to 9 % slower.  The reference's own
+    benchmark does the same through triton.testing.do_bench, whose warm-up is
+    25 ms of calls (rbf_attention.py:1877, 1888).
+  * `value` / `ms_per_step`: exactly K back-to-back steps between two HIP
+    events on the launch stream (warm caches: the step's ~205 MB working set
+    stays in the 256 MB MALL between steps).
+  * `cold`: the median over reps of one step timed alone after a 512 MiB
+    write that evicts L2 and MALL (outside the events).
+  * `kernel_us`: each kernel of the step in an event-timed loop of its own;
+    the roofline entry is computed from the dominant one.
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -26,6 +41,19 @@ if REPO not in sys.path:
 METRIC = "RBF-attn fwd+bwd TFLOP/s and % bf16 MFMA peak; train-step tokens/s"
 PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "fp32": 157.3}  # MI355X dense MFMA
 HBM_GBS = 8000.0
+FLUSH_MIB = 512  # > the 256 MB MALL + 8 x 4 MB L2
+
+# The reference's own benchmark sweep (rbf_attention.py:1768-1771, 1819-1911:
+# fp16, B=4, H=8, D=64, causal, torch.compile'd op, do_bench) and the values
+# its only published figure shows (outputs/attention_profiling_results.png,
+# read off the plot, +-3 %; the GPU is not recorded).
+REF_SWEEP = {"B": 4, "H": 8, "D": 64, "dtype": "fp16", "N": (1024, 2048, 4096, 8192)}
+REF_PUBLISHED = {
+    1024: {"fwd_ms": 0.13, "bwd_ms": 0.35, "peak_mb": 4.2},
+    2048: {"fwd_ms": 0.38, "bwd_ms": 1.07, "peak_mb": 8.3},
+    4096: {"fwd_ms": 1.28, "bwd_ms": 3.78, "peak_mb": 16.5},
+    8192: {"fwd_ms": 4.67, "bwd_ms": 14.25, "peak_mb": 33.0},
+}
 
 
 def log(*a):
@@ -151,6 +179,258 @@ def roofline(w, kernel: str, flops: float, seconds: float, peak_tflops: float):
     }
 
 
+class Timer:
+    """HIP-event timing on one stream, and an L2/MALL flush buffer."""
+
+    def __init__(self, torch, dev, stream):
+        self.torch, self.dev, self.stream = torch, dev, stream
+        self._flush = None
+
+    def loop(self, fn, n: int) -> float:
+        """Mean ms of n back-to-back calls between two events."""
+        torch = self.torch
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(self.stream)
+        for _ in range(n):
+            fn()
+        e1.record(self.stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    def flush(self):
+        if self._flush is None:
+            self._flush = self.torch.empty(FLUSH_MIB << 18, device=self.dev, dtype=self.torch.float32)
+        self._flush.fill_(1.0)
+
+    def cold(self, fn, reps: int, pre=None) -> list:
+        """ms of single calls, each after a cache-evicting write (and pre(),
+        e.g. resetting gradients), both outside the events."""
+        torch = self.torch
+        out = []
+        for _ in range(reps):
+            if pre is not None:
+                pre()
+            self.flush()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(self.stream)
+            fn()
+            e1.record(self.stream)
+            torch.cuda.synchronize()
+            out.append(e0.elapsed_time(e1))
+        return out
+
+    def ramp(self, fn, seconds: float) -> int:
+        """Runs fn untimed for about `seconds` (clock ramp); returns the count."""
+        n, t_end = 0, time.perf_counter() + seconds
+        while time.perf_counter() < t_end:
+            for _ in range(8):
+                fn()
+            n += 8
+            self.torch.cuda.synchronize()
+        return n
+
+
+def setup_workload(w, dev):
+    import torch
+
+    from rbf_attention_amd import _lib
+    from rbf_attention_amd import workloads as wl
+
+    q, k, v, do = (t.to(dev) for t in wl.make_inputs(w))
+    bufs = {"q": q, "k": k, "v": v, "dout": do}
+    for f in ("o", "dq", "dk", "dv"):
+        bufs[f] = torch.empty_like(q)
+    bufs["lse"] = torch.empty((w.B, w.H, w.N), device=dev, dtype=torch.float32)
+    bufs["delta"] = torch.empty_like(bufs["lse"])
+    variant = _lib.SOFTMAX if w.softmax else _lib.NON_SOFTMAX
+    return bufs, make_args(_lib, w, bufs, variant)
+
+
+def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold_reps: int, graph: bool):
+    """Step, per-kernel and cold-cache timings of one workload through the C
+    ABI; returns (result dict, step ms)."""
+    import torch
+
+    from rbf_attention_amd import _lib
+
+    bufs, a = setup_workload(w, dev)
+    sp = timer.stream.cuda_stream
+
+    def fwd():
+        _lib.call("rbf_attn_fwd", a, sp)
+
+    def bwd():
+        _lib.call("rbf_attn_bwd", a, sp)
+
+    def stage(s):
+        return lambda: _lib.call("rbf_attn_bwd_stage", a, sp, s)
+
+    def step():
+        fwd()
+        bwd()
+
+    ramp_n = timer.ramp(step, ramp_s)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    ms_step = timer.loop(step, steps)
+    wall = time.perf_counter() - wall0
+    log(f"{w.name}: step {ms_step * 1e3:.2f} us over {steps} steps (ramp {ramp_n} steps, wall {wall:.3f} s)")
+
+    cold = timer.cold(step, cold_reps)
+    cold_med = statistics.median(cold)
+    log(f"  cold step (after a {FLUSH_MIB} MiB write): median {cold_med * 1e3:.2f} us of {cold_reps}")
+
+    ms_graph = None
+    if graph:
+        # The same step captured once in a HIP graph and replayed; reported
+        # beside the eager step, not as it.
+        def cur_step():
+            s = torch.cuda.current_stream(dev).cuda_stream
+            _lib.call("rbf_attn_fwd", a, s)
+            _lib.call("rbf_attn_bwd", a, s)
+
+        try:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                cur_step()
+            g.replay()
+            ms_graph = timer.loop(g.replay, steps)
+            log(f"  graph step: {ms_graph * 1e3:.2f} us")
+        except RuntimeError as e:  # reported as null; the eager measurement stands
+            log(f"  graph step: capture failed ({e})")
+
+    # Per-kernel averages, each kernel in a loop of its own (events between
+    # single launches add their own cost to every launch).  With a one-launch
+    # backward its two stages are timed too, for reference.
+    bwd_launches = _lib.bwd_kernels(a)
+    step_kernels = ("fwd", "bwd") if bwd_launches == 1 else ("fwd", "bwd_dq", "bwd_dkdv")
+    calls = {"fwd": fwd, "bwd": bwd, "bwd_dq": stage(1), "bwd_dkdv": stage(2)}
+    timed_kernels = step_kernels + (("bwd_dq", "bwd_dkdv") if bwd_launches == 1 else ())
+    kern_ms = {kname: timer.loop(calls[kname], steps) for kname in timed_kernels}
+    for kname, t in kern_ms.items():
+        log(f"  {kname}: {t * 1e3:.2f} us/launch" + ("" if kname in step_kernels else " (stage alone)"))
+
+    P = w.visible_pairs() * w.B * w.H
+    per_pair = {"fwd": 4.0, "bwd_dq": 2.0, "bwd_dkdv": 8.0, "bwd": 10.0}  # algorithmic flop/pair/D per kernel
+    total = w.flops_fwd_bwd()
+    peak = PEAK_TFLOPS[w.dtype]
+    dom = max(step_kernels, key=kern_ms.get)
+    tflops = total / (ms_step * 1e-3) / 1e12
+    res = {
+        "step_us": round(ms_step * 1e3, 3),
+        "tflops": round(tflops, 3),
+        "pct_of_bf16_peak": round(100.0 * tflops / peak, 3),
+        "cold": {
+            "step_us_median": round(cold_med * 1e3, 3),
+            "tflops": round(total / (cold_med * 1e-3) / 1e12, 3),
+            "reps": cold_reps,
+            "flush": f"{FLUSH_MIB} MiB write before each rep, outside the events",
+        },
+        "graph_step_us": round(ms_graph * 1e3, 3) if ms_graph is not None else None,
+        "kernel_us": {kk: round(t * 1e3, 3) for kk, t in kern_ms.items()},
+        "step_kernels": list(step_kernels),
+        "roofline": roofline(w, dom, per_pair[dom] * w.D * P, kern_ms[dom] * 1e-3, peak),
+        "config": {
+            "workload": w.name, "B": w.B, "H": w.H, "N": w.N, "D": w.D, "dtype": w.dtype, "causal": w.causal,
+            "softmax": w.softmax, "gamma": w.sm_scale, "flops_per_step": total,
+        },
+    }
+    del bufs
+    return res, ms_step
+
+
+def peak_fwd_mb(dev, w) -> float:
+    """Peak memory the forward op allocates with autograd recording (its
+    saved output and L), as rbf_attention.py:1809-1816 measures it."""
+    import torch
+
+    import rbf_attention_amd as ra
+    from rbf_attention_amd import workloads as wl
+
+    q, k, v, _ = (t.to(dev).requires_grad_(True) for t in wl.make_inputs(w))
+    fn = ra.run_triton_rbf if w.softmax else ra.run_triton_non_softmax_rbf
+    out = fn(q, k, v, w.causal)  # first call outside the probe (library load)
+    del out
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    out = fn(q, k, v, w.causal)
+    peak = (torch.cuda.max_memory_allocated(dev) - base) / (1024 * 1024)
+    del out
+    return round(peak, 3)
+
+
+def reference_sweep(dev, timer, reps: int):
+    """The reference's own benchmark (rbf_attention.py:1819-1911) on our op:
+    fp16 B=4 H=8 D=64 causal, N = 1024..8192, gamma = 1/sqrt(D) through
+    run_triton_rbf (the rbf_attn_v5 ops and their autograd).  Like
+    triton.testing.do_bench: each rep is timed alone after a cache-evicting
+    write, gradients reset to None outside the events, mean over reps;
+    bwd = (fwd + bwd) - fwd (rbf_attention.py:1891)."""
+    import torch
+
+    import rbf_attention_amd as ra
+
+    c = REF_SWEEP
+    out = {"config": dict(c, N=list(c["N"]), causal=True, gamma="1/sqrt(D)", op="run_triton_rbf",
+                          timing=f"mean of {reps} reps, each after a {FLUSH_MIB} MiB write"), "rows": []}
+    for n in c["N"]:
+        g = torch.Generator().manual_seed(0)
+        shape = (c["B"], c["H"], n, c["D"])
+        q, k, v, do = (torch.randn(shape, generator=g).to(torch.float16).to(dev) for _ in range(4))
+        for t in (q, k, v):
+            t.requires_grad_(True)
+
+        def fwd():
+            with torch.no_grad():
+                ra.run_triton_rbf(q, k, v, True)
+
+        def fwd_bwd():
+            o = ra.run_triton_rbf(q, k, v, True)
+            o.backward(do)
+
+        def reset():
+            q.grad = k.grad = v.grad = None
+
+        for _ in range(3):
+            reset()
+            fwd_bwd()
+        timer.ramp(fwd, 0.05)
+        f_ms = statistics.fmean(timer.cold(fwd, reps))
+        fb_ms = statistics.fmean(timer.cold(fwd_bwd, reps, pre=reset))
+        reset()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats(dev)
+        base = torch.cuda.memory_allocated(dev)
+        o = ra.run_triton_rbf(q, k, v, True)
+        peak = (torch.cuda.max_memory_allocated(dev) - base) / (1024 * 1024)
+        del o
+        flops = 2.0 * c["B"] * c["H"] * n * n * c["D"]  # the figure's FA convention: causal fwd
+        pub = REF_PUBLISHED[n]
+        row = {
+            "N": n,
+            "fwd_ms": round(f_ms, 4),
+            "bwd_ms": round(fb_ms - f_ms, 4),
+            "peak_fwd_mb": round(peak, 2),
+            "fwd_tflops_fa": round(flops / (f_ms * 1e-3) / 1e12, 1),
+            "bwd_tflops_fa": round(2.5 * flops / ((fb_ms - f_ms) * 1e-3) / 1e12, 1),
+            "published": pub,
+            "speedup_vs_published": {"fwd": round(pub["fwd_ms"] / f_ms, 2), "bwd": round(pub["bwd_ms"] / (fb_ms - f_ms), 2)},
+        }
+        out["rows"].append(row)
+        log(f"  ref sweep N={n}: fwd {row['fwd_ms']} ms, bwd {row['bwd_ms']} ms, peak {row['peak_fwd_mb']} MB "
+            f"(published {pub})")
+        del q, k, v, do
+    return out
+
+
 def train_step_bench(dev, steps: int, warmup: int):
     """Benchmark config 5: one next-token training step (bf16 autocast fwd,
     bwd, AdamW) of the 8-layer d512 RBF transformer on synthetic tokens,
@@ -254,15 +534,20 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    # 300 warmup steps (~25 ms at C2): the first ~100 steps run up to 9 % slower
-    # while the GPU's clocks ramp up.
-    ap.add_argument("--warmup", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--ramp-seconds", type=float, default=0.4,
+                    help="untimed steps run for this long before the warmup steps (GPU clock ramp)")
+    ap.add_argument("--cold-reps", type=int, default=25)
     ap.add_argument("--workload", default="c2_model_bf16")
+    ap.add_argument("--quick", action="store_true",
+                    help="only the headline workload: no C3/C4 objects, reference sweep, train step or decode")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-train-step", action="store_true", help="skip the config-5 train-step measurement")
     ap.add_argument("--train-steps", type=int, default=20)
     ap.add_argument("--no-decode", action="store_true", help="skip the KV-cache decode measurement")
+    ap.add_argument("--no-extra-configs", action="store_true", help="skip the C3/C4 objects")
+    ap.add_argument("--no-ref-sweep", action="store_true", help="skip the reference's own fp16 length sweep")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="run one device copy of this many MiB before timing (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -273,38 +558,18 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+    if args.quick:
+        args.no_extra_configs = args.no_ref_sweep = args.no_train_step = args.no_decode = True
 
     import torch
 
-    from rbf_attention_amd import _lib
     from rbf_attention_amd import workloads as wl
 
     w = wl.CONFIGS[args.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    q, k, v, do = (t.to(dev) for t in wl.make_inputs(w))
-    bufs = {"q": q, "k": k, "v": v, "dout": do}
-    for f in ("o", "dq", "dk", "dv"):
-        bufs[f] = torch.empty_like(q)
-    bufs["lse"] = torch.empty((w.B, w.H, w.N), device=dev, dtype=torch.float32)
-    bufs["delta"] = torch.empty_like(bufs["lse"])
-    variant = _lib.SOFTMAX if w.softmax else _lib.NON_SOFTMAX
-    a = make_args(_lib, w, bufs, variant)
     stream = torch.cuda.current_stream(dev)
-    sp = stream.cuda_stream
-
-    def fwd():
-        _lib.call("rbf_attn_fwd", a, sp)
-
-    def bwd():
-        _lib.call("rbf_attn_bwd", a, sp)
-
-    def stage(s):
-        return lambda: _lib.call("rbf_attn_bwd_stage", a, sp, s)
-
-    def step():
-        fwd()
-        bwd()
+    timer = Timer(torch, dev, stream)
 
     if args.copy_probe_mb:
         src = torch.empty(args.copy_probe_mb << 18, device=dev, dtype=torch.float32).fill_(1.0)
@@ -314,68 +579,11 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
     log(f"workload {w.name}: B={w.B} H={w.H} N={w.N} D={w.D} {w.dtype} causal={w.causal} gamma={w.sm_scale:.6f}")
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    def timed(fn, n):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record(stream)
-        for _ in range(n):
-            fn()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / n  # ms
-
-    wall0 = time.perf_counter()
-    ms_step = timed(step, args.steps)
-    wall = time.perf_counter() - wall0
-    log(f"step: {ms_step * 1e3:.2f} us/step over {args.steps} steps (wall {wall:.3f} s)")
-
-    # The same step captured once in a HIP graph and replayed K times (no
-    # host launch cost per kernel); reported beside `value`, not as it.  On
-    # MI355X the replay measured slower than eager launches (C2 90 against
-    # 80 us), so the eager step is the one reported.
-    def cur_step():
-        s = torch.cuda.current_stream(dev).cuda_stream
-        _lib.call("rbf_attn_fwd", a, s)
-        _lib.call("rbf_attn_bwd", a, s)
-
-    ms_graph = None
-    try:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            cur_step()
-        graph.replay()
-        ms_graph = timed(graph.replay, args.steps)
-        log(f"graph step: {ms_graph * 1e3:.2f} us/step")
-    except RuntimeError as e:  # reported as null; the eager measurement stands
-        log(f"graph step: capture failed ({e})")
-
-    # Per-kernel averages: each kernel of the step timed in a loop of its own
-    # (events between single launches add their own cost to every launch).
-    # With a one-launch backward, its two stages are timed too, for reference.
-    bwd_launches = _lib.bwd_kernels(a)
-    step_kernels = ("fwd", "bwd") if bwd_launches == 1 else ("fwd", "bwd_dq", "bwd_dkdv")
-    calls = {"fwd": fwd, "bwd": bwd, "bwd_dq": stage(1), "bwd_dkdv": stage(2)}
-    timed_kernels = step_kernels + (("bwd_dq", "bwd_dkdv") if bwd_launches == 1 else ())
-    kern_ms = {kname: timed(calls[kname], args.steps) for kname in timed_kernels}
-    for kname, t in kern_ms.items():
-        log(f"  {kname}: {t * 1e3:.2f} us/launch" + ("" if kname in step_kernels else " (stage alone)"))
-
-    P = w.visible_pairs() * w.B * w.H
-    per_pair = {"fwd": 4.0, "bwd_dq": 2.0, "bwd_dkdv": 8.0, "bwd": 10.0}  # algorithmic flop/pair/D per kernel
-    total_flops = w.flops_fwd_bwd()
-    tflops = total_flops / (ms_step * 1e-3) / 1e12
-    peak = PEAK_TFLOPS[w.dtype]
-    dom = max(step_kernels, key=kern_ms.get)
-    dom_flops = per_pair[dom] * w.D * P
-
+    head, ms_step = measure_workload(w, dev, timer, args.steps, args.warmup, args.ramp_seconds, args.cold_reps,
+                                     graph=True)
     result = {
         "metric": METRIC,
-        "value": round(tflops, 3),
+        "value": head["tflops"],
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -386,23 +594,27 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": w.dtype,
         "data": "synthetic (seeded N(0,1) q/v/dO, lognormal-scaled keys, 4 zero register rows)",
-        "config": {
-            "workload": w.name,
-            "B": w.B,
-            "H": w.H,
-            "N": w.N,
-            "D": w.D,
-            "causal": w.causal,
-            "softmax": w.softmax,
-            "gamma": w.sm_scale,
-            "flops_per_step": total_flops,
-        },
-        "pct_of_bf16_peak": round(100.0 * tflops / peak, 3),
-        "graph_step_us": round(ms_graph * 1e3, 3) if ms_graph is not None else None,
-        "kernel_us": {kk: round(t * 1e3, 3) for kk, t in kern_ms.items()},
-        "step_kernels": list(step_kernels),
-        "roofline": roofline(w, dom, dom_flops, kern_ms[dom] * 1e-3, peak),
+        "config": head["config"],
+        "pct_of_bf16_peak": head["pct_of_bf16_peak"],
+        "clock_ramp_s": args.ramp_seconds,
+        "cold": head["cold"],
+        "graph_step_us": head["graph_step_us"],
+        "kernel_us": head["kernel_us"],
+        "step_kernels": head["step_kernels"],
+        "roofline": head["roofline"],
+        "peak_fwd_activation_mb": peak_fwd_mb(dev, w),
     }
+    if not args.no_extra_configs:
+        for name in ("c3_long_bf16", "c4_nonsoftmax_bf16"):
+            if name == w.name:
+                continue
+            r, _ = measure_workload(wl.CONFIGS[name], dev, timer, 20, 5, 0.2, 5, graph=False)
+            result[name.split("_")[0]] = r
+            torch.cuda.empty_cache()
+    if not args.no_ref_sweep:
+        log("reference sweep (fp16 B4 H8 D64, rbf_attention.py:1819-1911) ...")
+        result["reference_sweep"] = reference_sweep(dev, timer, 20)
+        torch.cuda.empty_cache()
     if not args.no_train_step:
         log("train step (config 5) ...")
         result["train_step"] = train_step_bench(dev, args.train_steps, 3)

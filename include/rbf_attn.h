@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define RBF_ATTN_ABI_VERSION 1
+#define RBF_ATTN_ABI_VERSION 2
 
 /* variant */
 #define RBF_ATTN_SOFTMAX 0
@@ -125,30 +125,42 @@ int rbf_attn_bwd(const rbf_attn_args* args, void* stream);
 int rbf_attn_bwd_stage(const rbf_attn_args* args, void* stream, int stage);
 
 /*
+ * A position term for rbf_attn_fwd_pos / rbf_attn_bwd_pos: a
+ * (batch, H, N, D) operand, with batch = B (one term per batch entry) or
+ * batch = 1 (one term shared by every batch entry, which the kernels read at
+ * every b: t.stride_b must then be 0).  Any other batch returns
+ * RBF_ATTN_EINVAL_SHAPE, and batch = 1 with t.stride_b != 0 returns
+ * RBF_ATTN_EINVAL_STRIDE, both before any launch: the kernels index the term
+ * with b * t.stride_b for every b < B, so a batch-1 term passed with its own
+ * nonzero batch stride would be read past its end.
+ */
+typedef struct rbf_attn_pos_term {
+  rbf_attn_tensor t;
+  int32_t batch;
+} rbf_attn_pos_term;
+
+/*
  * Forward / backward with a position term fused into the Q and K reads:
  * the kernels use q + pos and k + pos (each sum rounded to the element type,
  * as two separate elementwise adds of the tensors would store it) wherever
- * the plain entry points use q and k.  pos is a (B, H, N, D) operand like
- * the others: rows (b, h, n) of every b < B, h < H, n < N are read, so a
- * term shared by the batch (one (H, N, D) tensor) is passed with
- * stride_b = 0, never with the stride of its own batch-1 shape.  The
- * gradients dq, dk are those of the shifted inputs, which equal the
- * gradients of q, k; the term's own gradient is sum_b (dq + dk) and is left
- * to the caller.  No reference counterpart: it fuses the SuSiE position
- * embedding of the reference model (rbf_attention.py:1666-1688,
+ * the plain entry points use q and k.  The gradients dq, dk are those of the
+ * shifted inputs, which equal the gradients of q, k; the term's own gradient
+ * is sum_b (dq + dk) (batch = 1) or dq + dk (batch = B) and is left to the
+ * caller.  No reference counterpart: it fuses the SuSiE position embedding
+ * of the reference model (rbf_attention.py:1666-1688,
  * `q, k = q + pos_emb, k + pos_emb`) into the attention kernels.  Supported
  * for bf16/fp16, 32 < D <= 64, N <= 576 (the head-resident kernels);
  * otherwise RBF_ATTN_EUNSUPPORTED before any launch.
  */
-int rbf_attn_fwd_pos(const rbf_attn_args* args, const rbf_attn_tensor* pos, void* stream);
-int rbf_attn_bwd_pos(const rbf_attn_args* args, const rbf_attn_tensor* pos, void* stream);
+int rbf_attn_fwd_pos(const rbf_attn_args* args, const rbf_attn_pos_term* pos, void* stream);
+int rbf_attn_bwd_pos(const rbf_attn_args* args, const rbf_attn_pos_term* pos, void* stream);
 
 /* Number of kernels rbf_attn_bwd (pos == NULL) or rbf_attn_bwd_pos enqueues
  * for args: 1 (both passes of a head in one head-resident kernel), 2 (a dQ
  * kernel, then a dK/dV kernel), 0 for an empty problem, or a negative error
  * code for invalid args.  Launches nothing.  No reference counterpart: for
  * callers that time or profile the backward per kernel. */
-int rbf_attn_bwd_kernels(const rbf_attn_args* args, const rbf_attn_tensor* pos);
+int rbf_attn_bwd_kernels(const rbf_attn_args* args, const rbf_attn_pos_term* pos);
 
 /* 1 if rbf_attn_fwd_pos / rbf_attn_bwd_pos support args (shape, dtype), 0 if
  * not, or a negative error code for invalid args.  No reference counterpart. */

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be imported before the library is loaded)
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "librbfattn.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 SOFTMAX = 0
 NON_SOFTMAX = 1
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
@@ -56,6 +56,12 @@ class Tensor(ctypes.Structure):
         ("stride_h", ctypes.c_int64),
         ("stride_n", ctypes.c_int64),
     ]
+
+
+class PosTerm(ctypes.Structure):
+    """rbf_attn_pos_term: a (batch, H, N, D) position term, batch 1 or B."""
+
+    _fields_ = [("t", Tensor), ("batch", ctypes.c_int32)]
 
 
 class Args(ctypes.Structure):
@@ -151,11 +157,11 @@ def load(path: str | None = None):
         lib.rbf_attn_bwd.restype = ctypes.c_int
         lib.rbf_attn_bwd_stage.argtypes = [ctypes.POINTER(Args), ctypes.c_void_p, ctypes.c_int]
         lib.rbf_attn_bwd_stage.restype = ctypes.c_int
-        lib.rbf_attn_fwd_pos.argtypes = [ctypes.POINTER(Args), ctypes.POINTER(Tensor), ctypes.c_void_p]
+        lib.rbf_attn_fwd_pos.argtypes = [ctypes.POINTER(Args), ctypes.POINTER(PosTerm), ctypes.c_void_p]
         lib.rbf_attn_fwd_pos.restype = ctypes.c_int
-        lib.rbf_attn_bwd_pos.argtypes = [ctypes.POINTER(Args), ctypes.POINTER(Tensor), ctypes.c_void_p]
+        lib.rbf_attn_bwd_pos.argtypes = [ctypes.POINTER(Args), ctypes.POINTER(PosTerm), ctypes.c_void_p]
         lib.rbf_attn_bwd_pos.restype = ctypes.c_int
-        lib.rbf_attn_bwd_kernels.argtypes = [ctypes.POINTER(Args), ctypes.POINTER(Tensor)]
+        lib.rbf_attn_bwd_kernels.argtypes = [ctypes.POINTER(Args), ctypes.POINTER(PosTerm)]
         lib.rbf_attn_bwd_kernels.restype = ctypes.c_int
         lib.rbf_attn_pos_supported.argtypes = [ctypes.POINTER(Args)]
         lib.rbf_attn_pos_supported.restype = ctypes.c_int
@@ -184,6 +190,14 @@ def tensor_desc(t: torch.Tensor | None) -> Tensor:
     return Tensor(t.data_ptr(), s[0], s[1], s[2])
 
 
+def pos_desc(pos: torch.Tensor) -> PosTerm:
+    """Descriptor of a (1 or B, H, N, D) position term; a batch-1 term is
+    passed with stride_b = 0, as the library requires (it reads it at every b)."""
+    s = pos.stride()
+    batch = pos.shape[0]
+    return PosTerm(Tensor(pos.data_ptr(), 0 if batch == 1 else s[0], s[1], s[2]), batch)
+
+
 def decode_workspace_size(args: DecodeArgs) -> int:
     lib = load()
     n = lib.rbf_attn_decode_workspace_size(ctypes.byref(args))
@@ -208,7 +222,7 @@ def pos_supported(args: Args) -> bool:
     return rc == 1
 
 
-def bwd_kernels(args: Args, pos: Tensor | None = None) -> int:
+def bwd_kernels(args: Args, pos: PosTerm | None = None) -> int:
     """Kernels rbf_attn_bwd (or rbf_attn_bwd_pos with pos) enqueues for args."""
     lib = load()
     rc = lib.rbf_attn_bwd_kernels(ctypes.byref(args), ctypes.byref(pos) if pos is not None else None)
@@ -217,7 +231,7 @@ def bwd_kernels(args: Args, pos: Tensor | None = None) -> int:
     return rc
 
 
-def call_pos(fn_name: str, args, pos: Tensor, stream: int) -> None:
+def call_pos(fn_name: str, args, pos: PosTerm, stream: int) -> None:
     lib = load()
     rc = getattr(lib, fn_name)(ctypes.byref(args), ctypes.byref(pos), ctypes.c_void_p(stream))
     if rc != 0:

@@ -243,15 +243,21 @@ int rbf_attn_abi_version(void) { return RBF_ATTN_ABI_VERSION; }
 const char* rbf_attn_last_error(void) { return g_err; }
 
 // Checks a position term for rbf_attn_{fwd,bwd}_pos and stores it in p.
-static int set_pos(const rbf_attn_args* a, const rbf_attn_tensor* pos, rbf::Params& p) {
+static int set_pos(const rbf_attn_args* a, const rbf_attn_pos_term* pos, rbf::Params& p) {
   int rc;
   if (pos == nullptr) return fail(RBF_ATTN_EINVAL_PTR, "pos: null descriptor");
-  if ((rc = check_tensor("pos", *pos, elem_size(a->dtype)))) return rc;
+  if (pos->batch != 1 && pos->batch != a->B)
+    return fail(RBF_ATTN_EINVAL_SHAPE, "pos: batch extent %d must be 1 or B=%d", pos->batch, a->B);
+  if (pos->batch == 1 && a->B > 1 && pos->t.stride_b != 0)
+    return fail(RBF_ATTN_EINVAL_STRIDE,
+                "pos: a term shared by the batch (batch=1) must have stride_b = 0 (got %lld): it is read at every b",
+                (long long)pos->t.stride_b);
+  if ((rc = check_tensor("pos", pos->t, elem_size(a->dtype)))) return rc;
   if (rbf_attn_pos_supported(a) != 1)
     return fail(RBF_ATTN_EUNSUPPORTED, "position term fused only for bf16/fp16, 32 < D <= 64, N <= 576 (D=%d N=%d)", a->D,
                 a->N);
-  p.pos = pos->ptr;
-  copy_strides(p.spos, *pos);
+  p.pos = pos->t.ptr;
+  copy_strides(p.spos, pos->t);
   return RBF_ATTN_OK;
 }
 
@@ -261,7 +267,7 @@ int rbf_attn_pos_supported(const rbf_attn_args* a) {
   return (a->dtype != RBF_ATTN_FP32 && a->D > 32 && a->D <= 64 && a->N <= 576) ? 1 : 0;
 }
 
-static int fwd_impl(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* stream) {
+static int fwd_impl(const rbf_attn_args* a, const rbf_attn_pos_term* pos, void* stream) {
   int rc = check_common(a);
   if (rc) return rc;
   const size_t esz = elem_size(a->dtype);
@@ -284,7 +290,7 @@ static int fwd_impl(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* st
 }
 
 int rbf_attn_fwd(const rbf_attn_args* a, void* stream) { return fwd_impl(a, nullptr, stream); }
-int rbf_attn_fwd_pos(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* stream) {
+int rbf_attn_fwd_pos(const rbf_attn_args* a, const rbf_attn_pos_term* pos, void* stream) {
   if (pos == nullptr) {
     g_err[0] = '\0';
     return fail(RBF_ATTN_EINVAL_PTR, "pos: null descriptor");
@@ -292,7 +298,7 @@ int rbf_attn_fwd_pos(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* s
   return fwd_impl(a, pos, stream);
 }
 
-static int bwd_impl(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* stream, int stage) {
+static int bwd_impl(const rbf_attn_args* a, const rbf_attn_pos_term* pos, void* stream, int stage) {
   int rc = check_common(a);
   if (rc) return rc;
   if (stage < 0 || stage > 2) return fail(RBF_ATTN_EINVAL_ARGS, "unknown backward stage %d", stage);
@@ -343,7 +349,7 @@ static int bwd_impl(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* st
 
 int rbf_attn_bwd(const rbf_attn_args* a, void* stream) { return bwd_impl(a, nullptr, stream, 0); }
 
-int rbf_attn_bwd_pos(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* stream) {
+int rbf_attn_bwd_pos(const rbf_attn_args* a, const rbf_attn_pos_term* pos, void* stream) {
   if (pos == nullptr) {
     g_err[0] = '\0';
     return fail(RBF_ATTN_EINVAL_PTR, "pos: null descriptor");
@@ -351,7 +357,7 @@ int rbf_attn_bwd_pos(const rbf_attn_args* a, const rbf_attn_tensor* pos, void* s
   return bwd_impl(a, pos, stream, 0);
 }
 
-int rbf_attn_bwd_kernels(const rbf_attn_args* a, const rbf_attn_tensor* pos) {
+int rbf_attn_bwd_kernels(const rbf_attn_args* a, const rbf_attn_pos_term* pos) {
   int rc = check_common(a);
   if (rc) return rc;
   if ((long long)a->B * a->H * a->N == 0) return 0;

@@ -106,7 +106,7 @@ def _launch_pos(fn: str, a, pos: torch.Tensor, device: torch.device) -> None:
     if a.B * a.H * a.N == 0:
         return
     with torch.cuda.device(device):
-        _lib.call_pos(fn, a, _lib.tensor_desc(pos), torch.cuda.current_stream(device).cuda_stream)
+        _lib.call_pos(fn, a, _lib.pos_desc(pos), torch.cuda.current_stream(device).cuda_stream)
 
 
 def _check_pos(name: str, q: torch.Tensor, pos: torch.Tensor) -> None:
@@ -118,16 +118,16 @@ def _check_pos(name: str, q: torch.Tensor, pos: torch.Tensor) -> None:
 
 
 def _with_pos(name: str, a, q, k, pos, dp: int):
-    """Position term for a launch: the (B, H, N, dp) operand for the fused
-    entry points when the library fuses it for these args (the head-resident
-    kernels), else None after adding it to q and k here -- the same values
-    (each sum rounded to the element type), as separate elementwise adds."""
+    """Position term for a launch: the (1 or B, H, N, dp) operand for the
+    fused entry points when the library fuses it for these args (the
+    head-resident kernels), else None after adding it to q and k here -- the
+    same values (each sum rounded to the element type), as separate
+    elementwise adds."""
     if pos is None:
         return q, k, None
     _check_pos(name, q, pos)
     if _lib.pos_supported(a):
-        B, H, N, _ = q.shape
-        return q, k, _prep(pos, dp).expand(B, H, N, dp)
+        return q, k, _prep(pos, dp)
     return q + pos, k + pos, None
 
 

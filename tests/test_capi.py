@@ -58,7 +58,7 @@ FAKE = 0x10000  # aligned, never dereferenced: every call below fails validation
 
 def good_args(**over):
     a = _lib.Args()
-    a.abi_version = 1
+    a.abi_version = _lib.ABI_VERSION
     a.variant = 0
     a.dtype = 0
     a.B, a.H, a.N, a.D = 2, 3, 64, 64
@@ -82,7 +82,7 @@ def call(lib, fn, a):
 @pytest.mark.parametrize(
     "over,code",
     [
-        (dict(abi_version=2), -1),
+        (dict(abi_version=1), -1),
         (dict(variant=5), -1),
         (dict(dtype=7), -2),
         (dict(D=60), -4),
@@ -142,22 +142,62 @@ def test_pos_supported(lib):
     assert sup(dtype=7) == -2 and sup(D=60) == -4
 
 
+def pos_term(stride_b=0, batch=1, ptr=FAKE + 0x3000000):
+    return _lib.PosTerm(_lib.Tensor(ptr, stride_b, 64 * 64, 64), batch)
+
+
+def test_pos_struct_layout():
+    assert ctypes.sizeof(_lib.PosTerm) == 40 and _lib.PosTerm.batch.offset == 32
+
+
 def test_pos_entry_points_reject_before_launch(lib):
-    pos = _lib.Tensor(FAKE + 0x3000000, 0, 64 * 64, 64)
+    pos = pos_term()
     for fn in (lib.rbf_attn_fwd_pos, lib.rbf_attn_bwd_pos):
         assert fn(ctypes.byref(good_args()), None, None) == -6
         assert fn(ctypes.byref(good_args(D=128)), ctypes.byref(pos), None) == -8
         assert "576" in lib.rbf_attn_last_error().decode()
         assert fn(ctypes.byref(good_args(dtype=2)), ctypes.byref(pos), None) == -8
-        bad = _lib.Tensor(FAKE + 0x3000008, 0, 64 * 64, 64)
+        bad = pos_term(ptr=FAKE + 0x3000008)
         assert fn(ctypes.byref(good_args()), ctypes.byref(bad), None) == -3
         assert fn(ctypes.byref(good_args(N=0)), ctypes.byref(pos), None) == 0
+
+
+def test_pos_batch_extent(lib):
+    """A term shared by the batch (batch = 1) is read at every b, so it must
+    come with stride_b = 0: a batch-1 term passed with its own batch stride
+    would be read past its end.  Both misuses are rejected before any launch
+    (good_args has B = 2)."""
+    for fn in (lib.rbf_attn_fwd_pos, lib.rbf_attn_bwd_pos):
+        shared_with_stride = pos_term(stride_b=3 * 64 * 64, batch=1)
+        assert fn(ctypes.byref(good_args()), ctypes.byref(shared_with_stride), None) == -3
+        assert "stride_b" in lib.rbf_attn_last_error().decode()
+        for batch in (0, 3, -1):
+            assert fn(ctypes.byref(good_args()), ctypes.byref(pos_term(stride_b=64 * 64, batch=batch)), None) == -5
+            assert "batch" in lib.rbf_attn_last_error().decode()
+        # accepted descriptors (N = 0: validated, nothing launched)
+        assert fn(ctypes.byref(good_args(N=0)), ctypes.byref(pos_term(stride_b=0, batch=1)), None) == 0
+        assert fn(ctypes.byref(good_args(N=0)), ctypes.byref(pos_term(stride_b=3 * 64 * 64, batch=2)), None) == 0
+        # one batch entry: its stride is never used
+        assert fn(ctypes.byref(good_args(B=1, N=0)), ctypes.byref(pos_term(stride_b=7 * 64, batch=1)), None) == 0
+    n = lib.rbf_attn_bwd_kernels(ctypes.byref(good_args(N=516)), ctypes.byref(pos_term(stride_b=64, batch=1)))
+    assert n == -3
+
+
+def test_pos_desc_of_shared_term():
+    """The op layer's descriptor of a (1, H, N, D) term carries stride_b = 0
+    whatever the tensor's own batch stride is."""
+    t = torch.empty(1, 3, 64, 64)
+    d = _lib.pos_desc(t)
+    assert d.batch == 1 and d.t.stride_b == 0 and d.t.stride_h == 64 * 64
+    t2 = torch.empty(2, 3, 64, 64)
+    d2 = _lib.pos_desc(t2)
+    assert d2.batch == 2 and d2.t.stride_b == 3 * 64 * 64
 
 
 def test_bwd_kernels_query(lib):
     """Shapes decided without a device query: fp32 and D > 64 always take two
     launches, a fused position term on a head that fits takes one."""
-    pos = _lib.Tensor(FAKE + 0x3000000, 0, 64 * 64, 64)
+    pos = pos_term()
 
     def n(over, p=None):
         return lib.rbf_attn_bwd_kernels(ctypes.byref(good_args(**over)), ctypes.byref(p) if p else None)
