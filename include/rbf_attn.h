@@ -125,6 +125,24 @@ int rbf_attn_bwd(const rbf_attn_args* args, void* stream);
 int rbf_attn_bwd_stage(const rbf_attn_args* args, void* stream, int stage);
 
 /*
+ * Backward pass that allocates nothing and needs no caller workspace.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid allocation).  Same kernels and results as rbf_attn_bwd, but the fp32
+ * per-query workspace (softmax: Delta, in place of args->delta; non-softmax:
+ * the norm offsets, in place of args->lse) lives in a static device array of
+ * the library, one per GPU, held until the process ends.  args->delta is
+ * ignored; args->lse is read (the forward's L) for the softmax variant and
+ * ignored for the non-softmax one.  Limit: B * H * N <=
+ * RBF_ATTN_NOALLOC_MAX_ROWS (4 MiB of fp32 per GPU); larger problems return
+ * RBF_ATTN_EINVAL_SHAPE before any launch.  Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU (e.g. on two streams) race.
+ * The array needs no clearing: each call writes every entry it reads.
+ */
+#define RBF_ATTN_NOALLOC_MAX_ROWS (1 << 20)
+int rbf_attn_bwd_noalloc(const rbf_attn_args* args, void* stream);
+
+/*
  * A position term for rbf_attn_fwd_pos / rbf_attn_bwd_pos: a
  * (batch, H, N, D) operand, with batch = B (one term per batch entry) or
  * batch = 1 (one term shared by every batch entry, which the kernels read at

@@ -21,6 +21,7 @@ ABI_VERSION = 2
 SOFTMAX = 0
 NON_SOFTMAX = 1
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+NOALLOC_MAX_ROWS = 1 << 20  # RBF_ATTN_NOALLOC_MAX_ROWS: B*H*N limit of rbf_attn_bwd_noalloc
 
 ERRORS = {
     -1: "EINVAL_ARGS",
@@ -38,6 +39,7 @@ EXPORTS = (
     "rbf_attn_fwd",
     "rbf_attn_bwd",
     "rbf_attn_bwd_stage",
+    "rbf_attn_bwd_noalloc",
     "rbf_attn_fwd_pos",
     "rbf_attn_bwd_pos",
     "rbf_attn_bwd_kernels",
@@ -157,6 +159,8 @@ def load(path: str | None = None):
         lib.rbf_attn_bwd.restype = ctypes.c_int
         lib.rbf_attn_bwd_stage.argtypes = [ctypes.POINTER(Args), ctypes.c_void_p, ctypes.c_int]
         lib.rbf_attn_bwd_stage.restype = ctypes.c_int
+        lib.rbf_attn_bwd_noalloc.argtypes = [ctypes.POINTER(Args), ctypes.c_void_p]
+        lib.rbf_attn_bwd_noalloc.restype = ctypes.c_int
         lib.rbf_attn_fwd_pos.argtypes = [ctypes.POINTER(Args), ctypes.POINTER(PosTerm), ctypes.c_void_p]
         lib.rbf_attn_fwd_pos.restype = ctypes.c_int
         lib.rbf_attn_bwd_pos.argtypes = [ctypes.POINTER(Args), ctypes.POINTER(PosTerm), ctypes.c_void_p]

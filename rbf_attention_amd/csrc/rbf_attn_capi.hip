@@ -7,6 +7,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include <hip/hip_runtime.h>
 
 #include "rbf_attn.h"
@@ -177,6 +179,44 @@ int decode_check(const rbf_attn_decode_args* a, DecodeGeom* g) {
 
 }  // namespace
 
+// Workspace of rbf_attn_bwd_noalloc: one fp32 entry per (b, h, n) row.  The
+// host-side name `scratch` is only a stand-in for the symbol; the device
+// address of each GPU's copy comes from hipGetSymbolAddress (scratch_ptr).
+static __device__ __align__(256) float scratch[RBF_ATTN_NOALLOC_MAX_ROWS];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the GPU that runs `stream`, looked up once
+// per device with that device current.
+int scratch_ptr(hipStream_t stream, float** out) {
+  int dev = -1, cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return fail(RBF_ATTN_ELAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  dev = cur;
+  if (stream != nullptr && (e = hipStreamGetDevice(stream, &dev)) != hipSuccess)
+    return fail(RBF_ATTN_ELAUNCH, "hipStreamGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(RBF_ATTN_ELAUNCH, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess)
+      return fail(RBF_ATTN_ELAUNCH, "hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(RBF_ATTN_ELAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return RBF_ATTN_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 uint64_t rbf_attn_decode_workspace_size(const rbf_attn_decode_args* a) {
@@ -298,11 +338,19 @@ int rbf_attn_fwd_pos(const rbf_attn_args* a, const rbf_attn_pos_term* pos, void*
   return fwd_impl(a, pos, stream);
 }
 
-static int bwd_impl(const rbf_attn_args* a, const rbf_attn_pos_term* pos, void* stream, int stage) {
+// noalloc: the per-query workspace (softmax Delta, non-softmax norm offsets)
+// is the library's scratch array instead of args->delta / args->lse.
+static int bwd_impl(const rbf_attn_args* a, const rbf_attn_pos_term* pos, void* stream, int stage,
+                    bool noalloc = false) {
   int rc = check_common(a);
   if (rc) return rc;
   if (stage < 0 || stage > 2) return fail(RBF_ATTN_EINVAL_ARGS, "unknown backward stage %d", stage);
+  const long long rows = (long long)a->B * a->H * a->N;
+  if (noalloc && rows > RBF_ATTN_NOALLOC_MAX_ROWS)
+    return fail(RBF_ATTN_EINVAL_SHAPE, "B*H*N = %lld rows exceed the no-allocation workspace of %d rows", rows,
+                RBF_ATTN_NOALLOC_MAX_ROWS);
   const size_t esz = elem_size(a->dtype);
+  const bool softmax = a->variant == RBF_ATTN_SOFTMAX;
   if ((rc = check_tensor("q", a->q, esz))) return rc;
   if ((rc = check_tensor("k", a->k, esz))) return rc;
   if ((rc = check_tensor("v", a->v, esz))) return rc;
@@ -310,15 +358,23 @@ static int bwd_impl(const rbf_attn_args* a, const rbf_attn_pos_term* pos, void* 
   if ((rc = check_tensor("dq", a->dq, esz))) return rc;
   if ((rc = check_tensor("dk", a->dk, esz))) return rc;
   if ((rc = check_tensor("dv", a->dv, esz))) return rc;
-  if ((rc = check_f32("lse", a->lse))) return rc;
-  if (a->variant == RBF_ATTN_SOFTMAX) {
+  if ((softmax || !noalloc) && (rc = check_f32("lse", a->lse))) return rc;
+  if (softmax) {
     if ((rc = check_tensor("o", a->o, esz))) return rc;
-    if ((rc = check_f32("delta", a->delta))) return rc;
+    if (!noalloc && (rc = check_f32("delta", a->delta))) return rc;
   }
-  if ((long long)a->B * a->H * a->N == 0) return RBF_ATTN_OK;
+  if (rows == 0) return RBF_ATTN_OK;
   rbf::Params p = make_params(a);
   if (pos && (rc = set_pos(a, pos, p))) return rc;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (noalloc) {
+    float* ws = nullptr;
+    if ((rc = scratch_ptr(st, &ws))) return rc;
+    if (softmax)
+      p.delta = ws;
+    else
+      p.lse = ws;
+  }
   hipError_t e;
   if (stage == 0) {
     switch (a->dtype) {
@@ -348,6 +404,8 @@ static int bwd_impl(const rbf_attn_args* a, const rbf_attn_pos_term* pos, void* 
 }
 
 int rbf_attn_bwd(const rbf_attn_args* a, void* stream) { return bwd_impl(a, nullptr, stream, 0); }
+
+int rbf_attn_bwd_noalloc(const rbf_attn_args* a, void* stream) { return bwd_impl(a, nullptr, stream, 0, true); }
 
 int rbf_attn_bwd_pos(const rbf_attn_args* a, const rbf_attn_pos_term* pos, void* stream) {
   if (pos == nullptr) {

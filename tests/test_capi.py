@@ -123,6 +123,27 @@ def test_fp32_alignment(lib):
     assert call(lib, "rbf_attn_fwd", a) == -3
 
 
+def test_noalloc_validation(lib):
+    """rbf_attn_bwd_noalloc: same validation as rbf_attn_bwd, its workspace
+    pointers are not required, and problems beyond the static workspace are
+    rejected before any HIP call (nothing here reaches the device)."""
+    m = re.search(r"#define\s+RBF_ATTN_NOALLOC_MAX_ROWS\s+\(1 << (\d+)\)", open(HEADER).read())
+    assert m and (1 << int(m.group(1))) == _lib.NOALLOC_MAX_ROWS
+    f = lib.rbf_attn_bwd_noalloc
+    assert f(None, None) == -1
+    big = good_args(B=16, H=64, N=1025)  # 1,049,600 rows > 2^20
+    assert f(ctypes.byref(big), None) == -5
+    assert "workspace" in lib.rbf_attn_last_error().decode()
+    # at the limit: past the size check, stopped by the null q before any launch
+    assert f(ctypes.byref(good_args(B=16, H=64, N=1024, q=_lib.Tensor(None, 0, 0, 0))), None) == -6
+    assert f(ctypes.byref(good_args(D=60)), None) == -4
+    # workspaces: delta never needed; lse needed for softmax (the forward's L) only
+    assert f(ctypes.byref(good_args(N=0, delta=None)), None) == 0
+    assert f(ctypes.byref(good_args(N=0, delta=None, lse=None)), None) == -6
+    assert f(ctypes.byref(good_args(N=0, delta=None, lse=None, variant=1)), None) == 0
+    assert f(ctypes.byref(good_args(q=_lib.Tensor(None, 0, 0, 0))), None) == -6
+
+
 def test_empty_problem_is_noop(lib):
     for over in (dict(B=0), dict(H=0), dict(N=0)):
         assert call(lib, "rbf_attn_fwd", good_args(**over)) == 0
