@@ -18,6 +18,10 @@ It restates, in numpy float64, the reference's PyTorch math paths:
 * decode      the last T query rows of the causal forward over a KV cache
               (no reference counterpart; pinned to softmax_forward /
               non_softmax_forward)
+* rounding    rounded_model: the same math with P and dS rounded to the
+              element type where the reference kernels round them
+              (rbf_attention.py:201, 422, 432, 621) and outputs rounded; an
+              error-size reference for bf16/fp16 parity, not a target
 * augmented   q' = [q, 1, 0...], k' = [k, -||k||^2/2, 0...] padded to a
               multiple of 8, SDPA with scale 2*gamma  test_equivalence.py:9-33,
               rbf_math_test.py:46-64, rbf_attention.py:1718-1735
@@ -152,14 +156,89 @@ def non_softmax_backward(q, k, v, dO, gamma: float, causal: bool = True, num_pre
     return dQ, dK, dV
 
 
-def decode_forward(q, k, v, gamma: float, softmax: bool = True, lens=None):
+# ---------------------------------------------------------------------------
+# Rounding model of the reference kernels (error-size reference for bf16/fp16)
+# ---------------------------------------------------------------------------
+def round_bf16(x) -> np.ndarray:
+    """float64 -> nearest bfloat16 (ties to even, via float32) -> float64."""
+    x32 = np.ascontiguousarray(_f64(x), dtype=np.float32)
+    b = x32.view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFF0000
+    return b.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def round_fp16(x) -> np.ndarray:
+    return _f64(x).astype(np.float16).astype(np.float64)
+
+
+def rounder(dtype: str):
+    """Rounding to an element type named "bf16" / "fp16" / "fp32"."""
+    return {"bf16": round_bf16, "fp16": round_fp16,
+            "fp32": lambda x: _f64(x).astype(np.float32).astype(np.float64)}[dtype]
+
+
+def _identity(x):
+    return x
+
+
+def rounded_model(q, k, v, dO, gamma: float, softmax: bool = True, causal: bool = True, num_prefix: int = 0,
+                  rnd=_identity, out_rnd=_identity):
+    """(O, dQ, dK, dV) in float64 with the roundings the reference kernels
+    apply to their MFMA/dot operands, so that a kernel's error can be set
+    beside the error its own arithmetic makes unavoidable:
+
+    * P is rounded (``rnd``) before P V (rbf_attention.py:201) and P^T dO
+      (422); the forward's row sum uses the unrounded P (196-198); the
+      forward's P is taken relative to the row maximum (191-194), whose
+      power-of-two-free scale the rounding sees;
+    * dS is rounded before dS^T Q (432) and dS K (621); the key-norm column
+      sum of dK uses the unrounded dS (431, 447);
+    * Delta is formed from the stored (rounded) O (275-276);
+    * every output is rounded to the element type (``out_rnd``; 207-213,
+      447-460, 626-640).
+
+    Q/K pre-scaling in the element type (151, 361, 561) is not modelled (the
+    kernels here scale in fp32), so the model's error is a lower bound of
+    the reference kernel's.  With both roundings the identity this is exactly
+    softmax_forward/softmax_backward (non_softmax_*)."""
+    q, k, v, dO = _f64(q), _f64(k), _f64(v), _f64(dO)
+    N = q.shape[2]
+    vis = visibility(N, causal, num_prefix)
+    outs = [np.empty_like(x) for x in (v, q, k, v)]
+    for b, h, (qs, ks, vs, dos) in _slices(q, k, v, dO):
+        lg = np.where(vis, rbf_logits(qs, ks, gamma), -np.inf)
+        if softmax:
+            # the logits' -gamma||q||^2 is a per-row constant: P and dS are
+            # those of the kernels' 2 gamma q.k - gamma ||k||^2
+            ex = np.exp(lg - lg.max(axis=-1, keepdims=True))
+            den = ex.sum(axis=-1, keepdims=True)
+            o_st = out_rnd((rnd(ex) @ vs) / den)
+            prob = ex / den
+            grad_s = prob * (dos @ vs.T - (o_st * dos).sum(axis=-1, keepdims=True))
+            q_term = 0.0  # the q-norm-free logits have no d/dq of -gamma||q||^2
+        else:
+            prob = np.exp(lg)
+            o_st = out_rnd(rnd(prob) @ vs)
+            grad_s = prob * (dos @ vs.T)
+            q_term = grad_s.sum(axis=1)[:, None] * qs
+        r_gs = rnd(grad_s)
+        outs[0][b, h] = o_st
+        outs[1][b, h] = out_rnd(2.0 * gamma * (r_gs @ ks - q_term))
+        outs[2][b, h] = out_rnd(2.0 * gamma * (r_gs.T @ qs - grad_s.sum(axis=0)[:, None] * ks))
+        outs[3][b, h] = out_rnd(rnd(prob).T @ dos)
+    return tuple(outs)
+
+
+def decode_forward(q, k, v, gamma: float, softmax: bool = True, lens=None, rnd=_identity, out_rnd=_identity):
     """KV-cache decode: q (B,H,T,D) against caches k, v (B,H,L,D).  Query t of
     batch b sits at position lens[b] - T + t (lens defaults to L) and sees
     keys [0, that position]: rows lens[b]-T .. lens[b]-1 of the causal forward
     over the first lens[b] cached tokens (the reference has no decode path;
     this is its causal attention restricted to the last T query rows, with
     rbf_attention.py:1547-1553 logits).  Returns (O, L) in float64; L is the
-    base-2 LSE as in softmax_forward, and None for the non-softmax variant."""
+    base-2 LSE as in softmax_forward, and None for the non-softmax variant.
+    rnd / out_rnd: the rounding of P and of the output, as in rounded_model
+    (identity: exact)."""
     q, k, v = _f64(q), _f64(k), _f64(v)
     B, H, T, D = q.shape
     Lc = k.shape[2]
@@ -177,10 +256,10 @@ def decode_forward(q, k, v, gamma: float, softmax: bool = True, lens=None):
                 m = s.max(axis=-1, keepdims=True)
                 e = np.exp(s - m)
                 l = e.sum(axis=-1, keepdims=True)
-                O[b, h] = (e / l) @ v[b, h, :n]
+                O[b, h] = out_rnd((rnd(e) @ v[b, h, :n]) / l)
                 Lse[b, h] = (m[:, 0] + np.log(l[:, 0]) + gamma * np.einsum("td,td->t", q[b, h], q[b, h])) * LOG2E
             else:
-                O[b, h] = np.exp(s) @ v[b, h, :n]
+                O[b, h] = out_rnd(rnd(np.exp(s)) @ v[b, h, :n])
     return O, (Lse if softmax else None)
 
 

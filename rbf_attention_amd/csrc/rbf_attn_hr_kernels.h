@@ -181,10 +181,10 @@ __device__ inline int hr_block(int k, int wave, int W, int nblk, bool reverse) {
 // ---------------------------------------------------------------------------
 // Forward, head-resident.  The work-group loads the head's K and V (and
 // -0.5||k||^2) into LDS once; wave w then computes the output of its query
-// blocks as rbf_fwd_group does per block (static softmax bound with the row
-// sum on the MFMA path; online max for fp16, or as a per-block rerun when a
-// row's sum leaves [2^-60, 2^100]), reading K rows and transposed V from the
-// resident tiles.
+// blocks as rbf_fwd_group does per block (static softmax bound; O normalised
+// by the rounded P's sum from the MFMA path, L from the unrounded P's fp32
+// sum; online max for fp16, or as a per-block rerun when a row's sum leaves
+// [2^-60, 2^100]), reading K rows and transposed V from the resident tiles.
 //
 // Without a running max (static bound, non-softmax) the key loop is software
 // pipelined: iteration kb issues the S MFMAs of block kb+1 (K fragments and
@@ -272,13 +272,20 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
     // key blocks [0, kend) hold every key some query of the block sees
     const int kend = causal ? min(nblk, ((max(q0 + 31, npre - 1) - org) >> 5) + 1) : nblk;
 
-    f32x16_t oacc[ND], lacc;
+    f32x16_t oacc[ND], lacc;  // lacc row 0: sum of the rounded P
+    float lrow;  // this lane's share (16 of each block's 32 keys) of the unrounded P's sum
     float m_run;
-    // P = exp2(c S - m) for one block, then O^T += V^T P^T and l += 1^T P^T
+    // P = exp2(c S - m) for one block, then O^T += V^T P^T and l_r += 1^T P^T
+    // (P rounded to the element type) and l += sum P (fp32, unrounded)
     auto pv = [&](const f32x16_t& s, float moff, frag (*vA)[2]) {
       frag pf[2];
+      float pe[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) pf[i >> 3][i & 7] = (T)fast_exp2(fmaf(s[i], c, -moff));
+      for (int i = 0; i < 16; ++i) {
+        pe[i] = fast_exp2(fmaf(s[i], c, -moff));
+        pf[i >> 3][i & 7] = (T)pe[i];
+      }
+      if constexpr (SOFTMAX) lrow += tree_sum16(pe);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -290,6 +297,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
 #pragma unroll
       for (int d = 0; d < ND; ++d) oacc[d] = zero16();
       lacc = zero16();
+      lrow = 0.f;
       m_run = m0;
     };
 
@@ -312,6 +320,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
 #pragma unroll
             for (int d = 0; d < ND; ++d) oacc[d] *= alpha;
             lacc *= alpha;
+            lrow *= alpha;
             m_run = mnew;
           }
         }
@@ -365,13 +374,13 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
       }
     }
     if constexpr (STATIC) {
-      const float l = xhalf_sum(lacc[0]);
+      const float l = xhalf_sum(lrow);
       const bool bad = qvalid && !(l >= kSumLow && l <= kSumHigh);
       if (__any(bad)) run_safe();
     }
 
-    const float lsum = SOFTMAX ? xhalf_sum(lacc[0]) : 1.f;
-    const float inv = SOFTMAX ? 1.f / lsum : 1.f;
+    const float lsum = SOFTMAX ? xhalf_sum(lrow) : 1.f;
+    const float inv = SOFTMAX ? 1.f / xhalf_sum(lacc[0]) : 1.f;
     if (qvalid) {
       T* orow = O + (int64_t)qtok * p.so[2];
 #pragma unroll

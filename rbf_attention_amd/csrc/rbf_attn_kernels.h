@@ -700,9 +700,17 @@ __device__ inline f32x16_t splat16(float x) {
 // LDS.  Per 32-key block:
 //   S^T = K Q^T (accumulator initialised with -0.5||k||^2),
 //   P   = exp2(c S^T - m),
-//   O^T += V^T P^T, and l += 1^T P^T on the same MFMA path (an operand whose
-//   first row is ones), so the softmax denominator sums exactly the
-//   bf16-rounded P the numerator uses.
+//   O^T += V^T P^T with P rounded to the element type (as the reference
+//   rounds it before its P V product, rbf_attention.py:201),
+//   l_r += 1^T P^T on the same MFMA path (an operand whose first row is
+//   ones): O is normalised by the sum of exactly the rounded P its numerator
+//   uses, so a row that sees one key returns that key's v exactly;
+//   l += sum_j P in fp32 from the unrounded P, for L (the reference sums the
+//   unrounded P, 196-198).  L taken from l_r was off by up to 2^-9 relative
+//   per row, a scale every P of the backward then carried (dV's error at
+//   N = 32 was 1.2x that of the reference's own rounding); O normalised by
+//   the unrounded l was off by the rounding of the dominant P (the static
+//   offset below does not make it 1), e.g. O = v (1 + 2^-9) for one key.
 // Softmax offset m: every RBF logit obeys c(q.k - 0.5||k||^2) <= c 0.5||q||^2,
 // so m = c 0.5||q||^2 - 60 bounds P by 2^60 without any running max.  If some
 // row's keys all lie so far away that its sum falls below 2^-60 (or the sum is
@@ -776,7 +784,8 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
   qn2 = c * 0.5f * xhalf_sum(qn2);
   const frag onesA = ones_row_frag<T>(n);
 
-  f32x16_t oacc[ND], lacc;
+  f32x16_t oacc[ND], lacc;  // lacc row 0: sum of the rounded P
+  float lrow;  // this lane's share (16 of a block's 32 keys) of the unrounded P's sum
   float m_run;
 
   typedef TileFor<T, BN, DP, NT> TileT;
@@ -793,6 +802,7 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
 #pragma unroll
     for (int d = 0; d < ND; ++d) oacc[d] = zero16();
     lacc = zero16();
+    lrow = 0.f;
     m_run = !SOFTMAX ? qn2 : (SAFE ? -__builtin_inff() : qn2 - kBoundMargin);
     load_kv(0);
     for (int kt = 0; kt < nkt; ++kt) {
@@ -837,13 +847,19 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
 #pragma unroll
             for (int d = 0; d < ND; ++d) oacc[d] *= alpha;
             lacc *= alpha;
+            lrow *= alpha;
             m_run = mnew;
           }
         }
         const float moff = (SAFE && m_run == -__builtin_inff()) ? 0.f : m_run;
         frag pf[2];
+        float pe[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) pf[i >> 3][i & 7] = (T)fast_exp2(fmaf(s[i], c, -moff));
+        for (int i = 0; i < 16; ++i) {
+          pe[i] = fast_exp2(fmaf(s[i], c, -moff));
+          pf[i >> 3][i & 7] = (T)pe[i];
+        }
+        if constexpr (SOFTMAX) lrow += tree_sum16(pe);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -861,9 +877,7 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
     run(std::false_type{});
   }
   if constexpr (STATIC) {
-    // lacc row 0 (element 0 of the h = 0 lanes) is the row sum; the h = 1
-    // lanes hold row 4, which is zero.
-    const float l = xhalf_sum(lacc[0]);
+    const float l = xhalf_sum(lrow);
     const bool bad = qvalid && !(l >= kSumLow && l <= kSumHigh);
     if (__syncthreads_or(bad)) {
       __syncthreads();  // every wave is done reading the last tile
@@ -872,8 +886,10 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
   }
 
   if (!wave_on) return;
-  const float lsum = SOFTMAX ? xhalf_sum(lacc[0]) : 1.f;
-  const float inv = SOFTMAX ? 1.f / lsum : 1.f;
+  // lacc row 0 (element 0 of the h = 0 lanes) is the rounded P's sum; the
+  // h = 1 lanes hold row 4, which is zero.
+  const float inv = SOFTMAX ? 1.f / xhalf_sum(lacc[0]) : 1.f;
+  const float lsum = SOFTMAX ? xhalf_sum(lrow) : 1.f;
   if (qtok < 0) return;
   T* orow = O + (int64_t)qtok * p.so[2];
 #pragma unroll
@@ -1454,8 +1470,12 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
 //   barrier
 //   phase 2  P-wave:  dV^T += dO^T P
 //            dS-wave: dS = P dP with P from LDS, dK^T += Q^T dS, colsum += dS
-// The dS-wave takes P as rounded to the element type, the precision at which
-// P also enters dV.  SGB: every 32-query block issues all of its LDS operand
+// P reaches the dS-wave in fp32 (four float4 planes of 64 lanes each, so
+// every 16-byte LDS access of a wave is contiguous), as the one-wave kernels
+// form dS: dS and its column sum then carry no rounding of P, which only the
+// dV product sees (rounded to the element type, as in the reference).  With P
+// handed over in the element type instead, dK's relative L2 error at C3 was
+// 1.25x that of the reference's own rounding.  SGB: every 32-query block issues all of its LDS operand
 // reads before its MFMAs (sched_group_barrier), trading registers for hidden
 // LDS latency.
 // ---------------------------------------------------------------------------
@@ -1470,7 +1490,7 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
   __shared__ __attribute__((aligned(16))) T sD[2][TLy::SIZE];
   __shared__ __attribute__((aligned(16))) float sOff[2][BM];
   __shared__ __attribute__((aligned(16))) float sDel[2][BM];
-  __shared__ __attribute__((aligned(16))) T sP[NP][QB][2 * 64 * 8];
+  __shared__ __attribute__((aligned(16))) f32x4_t sP[NP][QB][4][64];
 
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1571,10 +1591,15 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
             __builtin_amdgcn_sched_group_barrier(0x008, KS, 0);
           }
           if (!blk_nomask(q0, k0, causal, npre)) mask_query_rows(s, q0, h, ilo);
+          f32x4_t pv[4];
 #pragma unroll
-          for (int i = 0; i < 16; ++i) pf[qb][i >> 3][i & 7] = (T)fast_exp2(fmaf(s[i], c, nckn));
-          st8<T>(sP[j][qb] + lane * 8, pf[qb][0]);
-          st8<T>(sP[j][qb] + (64 + lane) * 8, pf[qb][1]);
+          for (int i = 0; i < 16; ++i) {
+            const float e = fast_exp2(fmaf(s[i], c, nckn));
+            pv[i >> 2][i & 3] = e;
+            pf[qb][i >> 3][i & 7] = (T)e;
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) sP[j][qb][u][lane] = pv[u];
         }
         __syncthreads();
         // phase 2: dV^T += dO^T P
@@ -1613,12 +1638,14 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
           if (!act[qb]) continue;
-          const frag p0 = ld8<T>(sP[j][qb] + lane * 8), p1 = ld8<T>(sP[j][qb] + (64 + lane) * 8);
+          f32x4_t pv[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) pv[u] = sP[j][qb][u][lane];
           frag sf[2];
           float ds[16];
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            ds[i] = (float)(i < 8 ? p0[i] : p1[i - 8]) * dpacc[qb][i];
+            ds[i] = pv[i >> 2][i & 3] * dpacc[qb][i];
             sf[i >> 3][i & 7] = (T)ds[i];
           }
           csum += tree_sum16(ds);

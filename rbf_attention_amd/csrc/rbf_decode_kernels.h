@@ -142,8 +142,8 @@ __global__ __launch_bounds__(64 * W) void rbf_decode_split_kernel(const DecodePa
     float pv[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      pf[i >> 3][i & 7] = (T)fast_exp2(fmaf(s[i], c, -moff));
-      pv[i] = (float)pf[i >> 3][i & 7];  // the rounded P the numerator uses
+      pv[i] = fast_exp2(fmaf(s[i], c, -moff));  // the row sum takes P unrounded, as the forward does
+      pf[i >> 3][i & 7] = (T)pv[i];
     }
     if constexpr (SOFTMAX) lsum += tree_sum16(pv);
 #pragma unroll

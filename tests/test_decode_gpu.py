@@ -29,7 +29,11 @@ def run_case(q, k, v, softmax, gamma, lens=None, tag=""):
     out, lse = ra.rbf_decode(q, k, v, lt, softmax=softmax, sm_scale=gamma)
     torch.cuda.synchronize()
     O, L = ro.decode_forward(np64(q), np64(k), np64(v), gamma, softmax, lens)
-    check(f"{tag} O", out, O, q.dtype)
+    model = None
+    if q.dtype != torch.float32:
+        r = ro.rounder("bf16" if q.dtype == torch.bfloat16 else "fp16")
+        model, _ = ro.decode_forward(np64(q), np64(k), np64(v), gamma, softmax, lens, rnd=r, out_rnd=r)
+    check(f"{tag} O", out, O, q.dtype, kind="O", model=model)
     if softmax:
         err = float(np.abs(np64(lse) - L).max())
         print(f"{tag} L max_abs={err:.3e}", flush=True)

@@ -197,6 +197,118 @@ ALL_PINS = [
 ]
 
 
+# --- the rounding model (rounded_model) ---------------------------------------
+def pin_rounded_identity_limit(o, softmax=True, causal=True, num_prefix=0):
+    """Without rounding the model is the exact oracle."""
+    q, k, v, dO = rand(2, 2, 13, 8), rand(2, 2, 13, 8, scale=1.3), rand(2, 2, 13, 8), rand(2, 2, 13, 8)
+    g = 0.27
+    got = o.rounded_model(q, k, v, dO, g, softmax, causal, num_prefix)
+    if softmax:
+        ref = (o.softmax_forward(q, k, v, g, causal, num_prefix)[0],) + o.softmax_backward(q, k, v, dO, g, causal,
+                                                                                         num_prefix)
+    else:
+        ref = (o.non_softmax_forward(q, k, v, g, causal, num_prefix),) + o.non_softmax_backward(q, k, v, dO, g, causal,
+                                                                                              num_prefix)
+    return all(np.abs(a - b).max() < 1e-12 for a, b in zip(got, ref))
+
+
+def brute_rounded(q, k, v, dO, g, softmax, rnd, causal=True, num_prefix=0):
+    """Pure-Python loops of the reference kernels' arithmetic with a scalar
+    rounding at each point where they round to the element type: P before
+    P V and P^T dO, dS before dS^T Q and dS K, every stored output; row sums,
+    column sums and Delta's O read from the stored (rounded) output."""
+    q, k, v, dO = (np.asarray(x, dtype=np.float64).tolist() for x in (q, k, v, dO))
+    N, D = len(q), len(q[0])
+    r = lambda x: float(rnd(np.array([x]))[0])  # noqa: E731
+
+    def vis(i, j):
+        return (not causal) or j <= i or j < num_prefix
+
+    lg = [[-g * sum((q[i][d] - k[j][d]) ** 2 for d in range(D)) for j in range(N)] for i in range(N)]
+    P = [[0.0] * N for _ in range(N)]
+    O = [[0.0] * D for _ in range(N)]
+    for i in range(N):
+        if softmax:
+            mx = max(lg[i][j] for j in range(N) if vis(i, j))
+            e = [math.exp(lg[i][j] - mx) if vis(i, j) else 0.0 for j in range(N)]
+            den = sum(e)
+            for d in range(D):
+                O[i][d] = r(sum(r(e[j]) * v[j][d] for j in range(N)) / den)
+            P[i] = [x / den for x in e]
+        else:
+            P[i] = [math.exp(lg[i][j]) if vis(i, j) else 0.0 for j in range(N)]
+            for d in range(D):
+                O[i][d] = r(sum(r(P[i][j]) * v[j][d] for j in range(N)))
+    dS = [[0.0] * N for _ in range(N)]
+    for i in range(N):
+        dl = sum(O[i][d] * dO[i][d] for d in range(D)) if softmax else 0.0
+        for j in range(N):
+            dS[i][j] = P[i][j] * (sum(dO[i][d] * v[j][d] for d in range(D)) - dl)
+    dV = [[r(sum(r(P[i][j]) * dO[i][d] for i in range(N))) for d in range(D)] for j in range(N)]
+    dQ = [[r(2 * g * (sum(r(dS[i][j]) * k[j][d] for j in range(N))
+                      - (0.0 if softmax else sum(dS[i]) * q[i][d]))) for d in range(D)] for i in range(N)]
+    dK = [[r(2 * g * (sum(r(dS[i][j]) * q[i][d] for i in range(N)) - sum(dS[i][j] for i in range(N)) * k[j][d]))
+           for d in range(D)] for j in range(N)]
+    return O, dQ, dK, dV
+
+
+def pin_rounded_vs_brute(o, softmax=True, causal=True, num_prefix=0, dtype="bf16"):
+    """The vectorised model against the loops, with real bf16/fp16 rounding
+    (whose effects are ~2^-9 / 2^-11, far above float64 noise)."""
+    q, k, v, dO = rand(1, 1, 6, 5), rand(1, 1, 6, 5, scale=1.4), rand(1, 1, 6, 5), rand(1, 1, 6, 5)
+    g = 0.4
+    rnd = o.rounder(dtype)
+    got = o.rounded_model(q, k, v, dO, g, softmax, causal, num_prefix, rnd=rnd, out_rnd=rnd)
+    ref = brute_rounded(q[0, 0], k[0, 0], v[0, 0], dO[0, 0], g, softmax, rnd, causal, num_prefix)
+    return all(np.abs(a[0, 0] - np.array(b)).max() < 1e-12 for a, b in zip(got, ref))
+
+
+def pin_rounded_decode_vs_model(o, softmax=True):
+    """decode_forward with rounding equals the last T output rows of
+    rounded_model over the whole cache (full lengths)."""
+    q, k, v = rand(1, 2, 9, 8), rand(1, 2, 9, 8, scale=1.2), rand(1, 2, 9, 8)
+    g, T = 0.3, 3
+    r = o.rounder("bf16")
+    full = o.rounded_model(q, k, v, rand(1, 2, 9, 8), g, softmax, rnd=r, out_rnd=r)[0]
+    dec, _ = o.decode_forward(q[:, :, -T:], k, v, g, softmax, rnd=r, out_rnd=r)
+    return np.abs(dec - full[:, :, -T:]).max() < 1e-12
+
+
+ALL_PINS += [
+    lambda o: pin_rounded_decode_vs_model(o, True),
+    lambda o: pin_rounded_decode_vs_model(o, False),
+    lambda o: pin_rounded_identity_limit(o, True),
+    lambda o: pin_rounded_identity_limit(o, False),
+    lambda o: pin_rounded_identity_limit(o, True, True, 3),
+    lambda o: pin_rounded_identity_limit(o, False, False),
+    lambda o: pin_rounded_vs_brute(o, True),
+    lambda o: pin_rounded_vs_brute(o, False),
+    lambda o: pin_rounded_vs_brute(o, True, True, 2, "fp16"),
+    lambda o: pin_rounded_vs_brute(o, False, False, 0, "fp16"),
+]
+
+
+def test_rounding_helpers():
+    """bf16 / fp16 rounding against torch's own conversions (ties to even)."""
+    x = np.concatenate([rand(4000, scale=3.0), [1 / 3, 2 / 3, 1 + 2 ** -8, 1 + 3 * 2 ** -8, -7.2, 0.0]])
+    np.testing.assert_array_equal(ro.round_bf16(x), t64(x).to(torch.bfloat16).double().numpy())
+    np.testing.assert_array_equal(ro.round_fp16(x), t64(x).to(torch.float16).double().numpy())
+    assert ro.round_bf16(np.array([1 + 2 ** -8]))[0] == 1.0 and ro.round_bf16(np.array([1 + 3 * 2 ** -8]))[0] == 1 + 2 ** -6
+
+
+def test_rounded_model_error_is_bf16_sized():
+    """With bf16 rounding the model moves O by about the relative bf16
+    precision (2^-9 per rounded P, averaged over the row) -- and not by zero:
+    the rounding is really applied."""
+    q, k, v, dO = rand(1, 2, 64, 32), rand(1, 2, 64, 32), rand(1, 2, 64, 32), rand(1, 2, 64, 32)
+    g = 1 / (2 * math.sqrt(32))
+    exact = ro.rounded_model(q, k, v, dO, g)
+    model = ro.rounded_model(q, k, v, dO, g, rnd=ro.round_bf16, out_rnd=ro.round_bf16)
+    for a, b in zip(model, exact):
+        rel = np.linalg.norm(a - b) / np.linalg.norm(b)
+        assert 1e-4 < rel < 1e-2, rel
+
+
 @pytest.mark.parametrize("i", range(len(ALL_PINS)))
 def test_pin(i):
     assert ALL_PINS[i](ro)
@@ -288,6 +400,17 @@ MUTATIONS = {
     "augment_wrong_half": ("kp = np.concatenate([k, -0.5 * kk], axis=-1)", "kp = np.concatenate([k, -kk], axis=-1)"),
     "decode_position_off_by_one": ("pos = np.arange(n - T, n)[:, None]", "pos = np.arange(n - T - 1, n - 1)[:, None]"),
     "decode_ignores_lengths": ("lens = [Lc] * B if lens is None else [int(x) for x in lens]", "lens = [Lc] * B"),
+    # the rounding model: rounding at the wrong places, or a dropped term
+    "rounded_colsum_of_rounded_dS": ("grad_s.sum(axis=0)[:, None] * ks))", "r_gs.sum(axis=0)[:, None] * ks))"),
+    "rounded_dV_unrounded_P": ("out_rnd(rnd(prob).T @ dos)", "out_rnd(prob.T @ dos)"),
+    "rounded_delta_from_unstored_O": ("(o_st * dos).sum(axis=-1, keepdims=True)",
+                                      "((rnd(ex) @ vs) / den * dos).sum(axis=-1, keepdims=True)"),
+    "rounded_row_sum_of_rounded_P": ("den = ex.sum(axis=-1, keepdims=True)", "den = rnd(ex).sum(axis=-1, keepdims=True)"),
+    "rounded_nonsoftmax_dQ_norm_term": ("q_term = grad_s.sum(axis=1)[:, None] * qs", "q_term = 0.0"),
+    "rounded_decode_unrounded_P": ("out_rnd(rnd(np.exp(s)) @ v[b, h, :n])", "out_rnd(np.exp(s) @ v[b, h, :n])"),
+    "rounded_decode_row_sum_of_rounded_P": ("out_rnd((rnd(e) @ v[b, h, :n]) / l)",
+                                            "out_rnd((rnd(e) @ v[b, h, :n]) / rnd(e).sum(axis=-1, keepdims=True))"),
+    "rounded_dQ_unrounded_dS": ("out_rnd(2.0 * gamma * (r_gs @ ks - q_term))", "out_rnd(2.0 * gamma * (grad_s @ ks - q_term))"),
 }
 
 

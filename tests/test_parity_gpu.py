@@ -1,16 +1,29 @@
 """GPU parity of the HIP kernels against the CPU oracle (float64 restatement
 of the reference math, oracle/rbf_oracle.py) on identical seeded inputs.
 
-Tolerances (from the build's target):
+Tolerances (plus what storing a result in bf16 and the
+reference kernels' own roundings make unavoidable):
   * fp32 inputs: max-abs error <= 1e-4 on O, dQ, dK, dV.
-  * bf16 / fp16 inputs: relative L2 error <= 1e-2, and
-    max |got - ref| <= 2e-2 + 2^-7 max|ref|.  The second term is one bf16 ulp
-    of the tensor's largest magnitude: storing a result of magnitude >= 8 in
-    bf16 alone moves it by up to 2^-8 of its value (more than 2e-2), and
-    P / dS enter the MFMAs rounded to bf16 exactly as in the reference
-    kernels (rbf_attention.py:201, 422, 432, 621).  A bound per element
-    would be wrong for dK = 2g(dS^T Q - colsum(dS) k), whose small entries
-    come from the cancellation of large terms.  The literal max-abs is logged.
+  * bf16 / fp16 inputs, every tensor: relative L2 error <= 1e-2.
+  * O and dV, elementwise: |got - ref| <= 2e-2 + half an ulp of |ref| in the
+    element type (storing a value of magnitude >= 8 in bf16 alone moves it by
+    up to 2^-5 > 2e-2).  Where the rounding model below misses that bound on
+    some elements (C4: ~2000-term unnormalised sums of bf16-rounded P), the
+    kernel may miss it on at most 1.25x as many.
+  * dQ and dK, tensor-wide: max |got - ref| <= 2e-2 + 2^-7 max|ref|.  An
+    elementwise bound would be wrong for dK = 2g(dS^T Q - colsum(dS) k), whose
+    small entries come from the cancellation of large terms.
+  * Against the rounding model (oracle.rbf_oracle.rounded_model: the exact
+    math with P and dS rounded to the element type where the reference
+    kernels round them, rbf_attention.py:201, 422, 432, 621, and outputs
+    rounded): the kernel's relative L2 error is at most 1.2x the model's, on
+    tensors of >= 4096 elements (fewer make the ratio noisy).  So the
+    kernels' errors are those of the reference's own arithmetic, not more.
+    Not for dQ/dK of the far-query cases: with |q| ~ 48 their dK amplifies
+    the output rounding of a few rows' O (through Delta) by |q|, so one
+    realization of that rounding against another differs by up to ~1.4x (a
+    CPU backward fed the kernel's own O and L reproduces its dK exactly, and
+    the kernel's per-row O and Delta errors are distributed as the model's).
   * A reference that is identically zero (dQ for N = 1: one visible key,
     dS = 0) is checked with max-abs <= 1e-5 instead of a relative norm.
   * dQ and dK at N <= 2 are checked at rel-L2 <= 3e-2: with one or two
@@ -37,33 +50,69 @@ from rbf_attention_amd import workloads as wl
 pytestmark = pytest.mark.gpu
 
 ULP_BF16 = 2.0 ** -7
+DTYPE_NAMES = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}
+MODEL_RATIO = 1.2  # kernel rel-L2 error / rounding model's, at most
+MODEL_MIN_ELEMS = 4096
 
 
 def np64(t):
     return t.detach().to("cpu", torch.float64).numpy()
 
 
-def check(name, got, ref, dtype, rel_l2_max=1e-2):
-    got = np64(got)
+def half_ulp(x, dtype):
+    """Half the spacing of the element type's numbers at |x| (0 at x = 0)."""
+    mant = 10 if dtype == torch.float16 else 7
+    a = np.abs(x)
+    e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    return np.where(a > 0, np.exp2(e - mant - 1), 0.0)
+
+
+def errors(got, ref, dtype, elementwise):
     err = np.abs(got - ref)
     ref_norm = np.linalg.norm(ref)
-    rel_l2 = np.linalg.norm(got - ref) / ref_norm if ref_norm > 0 else float("nan")
-    max_abs = float(err.max()) if err.size else 0.0
-    info = f"{name}: max_abs={max_abs:.3e} rel_l2={rel_l2:.3e} max|ref|={np.abs(ref).max() if ref.size else 0:.3e}"
+    out = {
+        "max_abs": float(err.max()) if err.size else 0.0,
+        "rel_l2": float(np.linalg.norm(got - ref) / ref_norm) if ref_norm > 0 else float("nan"),
+        "max_ref": float(np.abs(ref).max()) if ref.size else 0.0,
+    }
+    if elementwise and err.size:
+        out["n_viol"] = int((err > 2e-2 + half_ulp(ref, dtype)).sum())
+    return out
+
+
+def check(name, got, ref, dtype, rel_l2_max=1e-2, kind=None, model=None, model_ratio=True):
+    """kind: "O"/"dV" (elementwise bound), "dQ"/"dK" (tensor-wide bound), or
+    None (tensor-wide, for comparisons against something other than the
+    oracle); model: the rounding model's output for the same inputs, whose
+    error the kernel's may exceed by MODEL_RATIO at most (if model_ratio)."""
+    got = np64(got)
+    elementwise = kind in ("O", "dV") and dtype != torch.float32
+    e = errors(got, ref, dtype, elementwise)
+    m = errors(model, ref, dtype, elementwise) if model is not None else None
+    info = (f"{name}: max_abs={e['max_abs']:.3e} rel_l2={e['rel_l2']:.3e} max|ref|={e['max_ref']:.3e}"
+            + (f" viol={e['n_viol']}" if elementwise else "")
+            + (f" | model max_abs={m['max_abs']:.3e} rel_l2={m['rel_l2']:.3e}"
+               + (f" viol={m['n_viol']}" if elementwise else "") if m else ""))
     print(info, flush=True)
     log = os.environ.get("RBF_PARITY_LOG")
     if log:
         with open(log, "a") as f:
-            f.write(json.dumps({"name": name, "dtype": str(dtype), "max_abs": max_abs, "rel_l2": rel_l2,
-                                "max_ref": float(np.abs(ref).max()) if ref.size else 0.0}) + "\n")
+            f.write(json.dumps({"name": name, "dtype": str(dtype), **e, "model": m}) + "\n")
     assert np.isfinite(got).all(), f"{name}: non-finite values"
     if dtype == torch.float32:
-        assert max_abs <= 1e-4, info
-    elif ref_norm == 0:
-        assert max_abs <= 1e-5, info
+        assert e["max_abs"] <= 1e-4, info
+        return
+    if not np.linalg.norm(ref) > 0:
+        assert e["max_abs"] <= 1e-5, info
+        return
+    assert e["rel_l2"] <= rel_l2_max, info
+    if elementwise:
+        allowed = 0 if m is None else math.ceil(1.25 * m["n_viol"])
+        assert e["n_viol"] <= allowed, info
     else:
-        assert rel_l2 <= rel_l2_max, info
-        assert max_abs <= 2e-2 + ULP_BF16 * float(np.abs(ref).max()), info
+        assert e["max_abs"] <= 2e-2 + ULP_BF16 * e["max_ref"], info
+    if m is not None and model_ratio and ref.size >= MODEL_MIN_ELEMS:
+        assert e["rel_l2"] <= MODEL_RATIO * m["rel_l2"] + 1e-6, info
 
 
 def run_ours(q, k, v, do, softmax, causal, gamma, num_prefix):
@@ -75,29 +124,44 @@ def run_ours(q, k, v, do, softmax, causal, gamma, num_prefix):
     return out, q.grad, k.grad, v.grad
 
 
-def oracle_all(q, k, v, do, softmax, causal, gamma, num_prefix, sl=None):
+def oracle_all(q, k, v, do, softmax, causal, gamma, num_prefix, sl=None, with_model=False):
+    """(O, dQ, dK, dV) of the float64 oracle, its L (softmax), and -- when
+    with_model and the inputs are 16-bit -- the rounding model's outputs."""
     arrs = [np64(t) for t in (q, k, v, do)]
     if sl is not None:
         arrs = [a[sl] for a in arrs]
     qn, kn, vn, don = arrs
     if softmax:
         O, L = ro.softmax_forward(qn, kn, vn, gamma, causal, num_prefix)
-        g = ro.softmax_backward(qn, kn, vn, don, gamma, causal, num_prefix)
-        return (O,) + g, L
-    O = ro.non_softmax_forward(qn, kn, vn, gamma, causal, num_prefix)
-    return (O,) + ro.non_softmax_backward(qn, kn, vn, don, gamma, causal, num_prefix), None
+        refs = (O,) + ro.softmax_backward(qn, kn, vn, don, gamma, causal, num_prefix)
+    else:
+        O, L = ro.non_softmax_forward(qn, kn, vn, gamma, causal, num_prefix), None
+        refs = (O,) + ro.non_softmax_backward(qn, kn, vn, don, gamma, causal, num_prefix)
+    model = None
+    if with_model and q.dtype != torch.float32:
+        r = ro.rounder(DTYPE_NAMES[q.dtype])
+        model = ro.rounded_model(qn, kn, vn, don, gamma, softmax, causal, num_prefix, rnd=r, out_rnd=r)
+    return refs, L, model
 
 
-def compare_case(q, k, v, do, softmax=True, causal=True, gamma=None, num_prefix=0, sl=None, tag=""):
+def compare_case(q, k, v, do, softmax=True, causal=True, gamma=None, num_prefix=0, sl=None, tag="", outs=None,
+                 ill_conditioned=False):
+    """Runs the kernels (unless their outputs are given) and checks O, dQ, dK,
+    dV -- on the (b, h) slices sl, if given -- against the oracle.
+    ill_conditioned: queries far from every key (see the module docstring):
+    no rounding-model ratio for dQ and dK."""
     D = q.shape[-1]
     g = gamma if gamma is not None else 1.0 / math.sqrt(D)
     print(f"case {tag} shape={tuple(q.shape)} {q.dtype} softmax={softmax} causal={causal} "
           f"gamma={g:.5f} num_prefix={num_prefix}", flush=True)
-    outs = run_ours(q, k, v, do, softmax, causal, gamma, num_prefix)
-    refs, _ = oracle_all(q, k, v, do, softmax, causal, g, num_prefix, sl)
-    for name, got, ref in zip(("O", "dQ", "dK", "dV"), outs, refs):
+    if outs is None:
+        outs = run_ours(q, k, v, do, softmax, causal, gamma, num_prefix)
+    refs, _, model = oracle_all(q, k, v, do, softmax, causal, g, num_prefix, sl, with_model=True)
+    for i, (name, got, ref) in enumerate(zip(("O", "dQ", "dK", "dV"), outs, refs)):
         rel = 3e-2 if (name in ("dQ", "dK") and q.shape[2] <= 2) else 1e-2
-        check(f"{tag} {name}", got if sl is None else got[sl], ref, q.dtype, rel)
+        check(f"{tag} {name}", got if sl is None else got[sl], ref, q.dtype, rel, kind=name,
+              model=None if model is None else model[i],
+              model_ratio=not (ill_conditioned and name in ("dQ", "dK")))
     return outs
 
 
@@ -145,22 +209,41 @@ def test_c2_registers_visible_to_all(cuda_device):
     compare_case(q, k, v, do, gamma=w.sm_scale, num_prefix=4, tag="C2-prefix4")
 
 
-def test_c3_long_bf16_sampled(cuda_device):
-    w = wl.C3_LONG
-    q, k, v, do = to_dev(wl.make_inputs(w), cuda_device)
-    sl = (slice(1, 2), slice(5, 6))  # one (b, h) slice checked against the oracle
-    outs = compare_case(q, k, v, do, gamma=w.sm_scale, sl=sl, tag="C3")
-    # full-size properties: finite everywhere; the zero register row 0 sees only
-    # key 0 (v_0 = 0), so O[:, :, 0] == 0 exactly.
+_C3 = {}
+
+
+def c3_outputs(dev):
+    """C3 inputs and kernel outputs, computed once for the slice checks."""
+    if not _C3:
+        w = wl.C3_LONG
+        q, k, v, do = to_dev(wl.make_inputs(w), dev)
+        _C3["inputs"] = (q, k, v, do)
+        _C3["outs"] = run_ours(q, k, v, do, True, True, w.sm_scale, 0)
+    return _C3["inputs"], _C3["outs"]
+
+
+@pytest.mark.parametrize("b,h", [(0, 0), (1, 5), (2, 10), (3, 15)])
+def test_c3_long_bf16_sampled(cuda_device, b, h):
+    """Four (b, h) slices of C3 against the oracle, the last head included."""
+    (q, k, v, do), outs = c3_outputs(cuda_device)
+    sl = (slice(b, b + 1), slice(h, h + 1))
+    compare_case(q, k, v, do, gamma=wl.C3_LONG.sm_scale, sl=sl, tag=f"C3 b{b}h{h}", outs=outs)
+
+
+def test_c3_long_bf16_full_size_properties(cuda_device):
+    """Finite everywhere; the zero register row 0 sees only key 0 (v_0 = 0),
+    so O[:, :, 0] == 0 exactly."""
+    _, outs = c3_outputs(cuda_device)
     for t in outs:
         assert torch.isfinite(t).all()
     assert (outs[0][:, :, 0] == 0).all()
+    _C3.clear()
 
 
 def test_c4_nonsoftmax_bf16_sampled(cuda_device):
     w = wl.C4_NONSOFTMAX
     q, k, v, do = to_dev(wl.make_inputs(w), cuda_device)
-    sl = (slice(0, 16, 5), slice(0, 8, 3))  # 4 x 3 slices
+    sl = (slice(1, 16, 2), slice(1, 8, 3))  # 8 x 3 = 24 slices, the last (b, h) = (15, 7) included
     outs = compare_case(q, k, v, do, softmax=False, gamma=w.sm_scale, sl=sl, tag="C4")
     for t in outs:
         assert torch.isfinite(t).all()
@@ -223,7 +306,7 @@ def test_queries_far_from_every_key(cuda_device, dtype, shift):
     q, k, v, do = rand_inputs(2, 4, 200, 64, dtype, cuda_device, seed=17)
     q = q.clone()
     q[:, ::2, :90] += shift
-    compare_case(q, k, v, do, gamma=0.0625, tag=f"far{shift} {dtype}")
+    compare_case(q, k, v, do, gamma=0.0625, tag=f"far{shift} {dtype}", ill_conditioned=True)
 
 
 @pytest.mark.parametrize(
@@ -257,7 +340,8 @@ def test_head_resident_shapes(cuda_device, N, D, dtype, softmax, causal, num_pre
         q = q.clone()
         q[:2, ::2, :90] += shift
     compare_case(q, k, v, do, softmax=softmax, causal=causal, num_prefix=num_prefix, gamma=1.0 / (2 * math.sqrt(D)),
-                 sl=(slice(0, 2), slice(0, 2)), tag=f"hr N{N} D{D} {dtype} sm{softmax} c{causal} p{num_prefix} far{shift}")
+                 sl=(slice(0, 2), slice(0, 2)), tag=f"hr N{N} D{D} {dtype} sm{softmax} c{causal} p{num_prefix} far{shift}",
+                 ill_conditioned=shift > 0)
 
 
 @pytest.mark.parametrize("causal", [True, False])
@@ -282,7 +366,7 @@ def test_flex_attention_cross_check(cuda_device, causal):
     of.backward(do.float())
     torch.cuda.synchronize()
     flex = (of, qf.grad, kf.grad, vf.grad)
-    refs, _ = oracle_all(q, k, v, do, True, causal, g, 0)
+    refs, _, _ = oracle_all(q, k, v, do, True, causal, g, 0)
     for name, a, f, r in zip(("O", "dQ", "dK", "dV"), ours, flex, refs):
         check(f"flex c{causal} {name} (ours vs flex)", a, np64(f), q.dtype)
         fe = float(np.abs(np64(f) - r).max())

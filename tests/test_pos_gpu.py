@@ -73,3 +73,52 @@ def test_pos_small_batch_and_fallback(cuda_device, B, H, D):
         x, y = x.double(), y.double()
         rel = ((x - y).norm() / y.norm()).item()
         assert rel <= 1e-2, f"{name}: rel_l2 {rel:.3e}"
+
+
+def test_pos_against_oracle_c5_shape(cuda_device):
+    """The model's shape (config 5: B*H = 256 heads, N = 512 + 4 registers,
+    D = 64, bf16, a SuSiE-like term shared by the batch, token-major output,
+    the reference's gamma = 1/sqrt(D)) against the float64 oracle evaluated on
+    bf16(q + P) and bf16(k + P) (the sums the model's separate adds would
+    store, rbf_attention.py:1666-1688): O, dQ, dK, dV on six (b, h) slices,
+    and the term's gradient dP = sum_b (dq + dk) on two heads (all 32 batch
+    entries each)."""
+    import numpy as np
+
+    from oracle import rbf_oracle as ro
+    from test_parity_gpu import check, np64
+
+    B, H, N, D = 32, 8, 516, 64
+    gamma = 1.0 / math.sqrt(D)
+    q, k, v, do, _ = inputs(B, H, N, D, torch.bfloat16, cuda_device, seed=5)
+    g = torch.Generator().manual_seed(6)
+    t = torch.arange(N - 4, dtype=torch.float32)[:, None] / (10000.0 ** (torch.arange(0, D, 2) / D))
+    sus = torch.cat([t.sin(), t.cos()], -1)  # the SuSiE table, rows 4..N-1
+    P = torch.cat([torch.randn(H, 4, D, generator=g) * 0.02, sus.expand(H, N - 4, D)], 1)[None]
+    P = P.to(torch.bfloat16).to(cuda_device)
+    a = _lib.Args()
+    a.abi_version, a.variant, a.dtype = _lib.ABI_VERSION, 0, _lib.DTYPE_CODES[torch.bfloat16]
+    a.B, a.H, a.N, a.D, a.causal, a.gamma = B, H, N, D, 1, gamma
+    assert _lib.pos_supported(a)
+    qq, kk, vv, pp = (x.clone().requires_grad_(True) for x in (q, k, v, P))
+    out = ra.run_triton_rbf(qq, kk, vv, True, pos=pp, token_major=True)
+    assert out.transpose(1, 2).is_contiguous()
+    out.backward(do)
+    torch.cuda.synchronize()
+    qs, ks = (q + P), (k + P)  # rounded to bf16, as the model's adds store them
+    r = ro.rounder("bf16")
+    for b, h in ((0, 0), (5, 2), (13, 4), (20, 1), (27, 6), (31, 7)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        arr = [np64(x)[sl] for x in (qs, ks, v, do)]
+        O, _ = ro.softmax_forward(arr[0], arr[1], arr[2], gamma)
+        grads = ro.softmax_backward(*arr, gamma)
+        model = ro.rounded_model(*arr, gamma, rnd=r, out_rnd=r)
+        for i, (name, got, ref) in enumerate(zip(("O", "dQ", "dK", "dV"), (out, qq.grad, kk.grad, vv.grad),
+                                                 (O,) + grads)):
+            check(f"pos C5 b{b}h{h} {name}", got[sl], ref, torch.bfloat16, kind=name, model=model[i])
+    for h in (0, 7):
+        arr = [np64(x)[:, h:h + 1] for x in (qs, ks, v, do)]
+        dq, dk, _ = ro.softmax_backward(*arr, gamma)
+        dP = (dq + dk).sum(axis=0, keepdims=True)
+        check(f"pos C5 dP h{h}", pp.grad[:, h:h + 1], dP, torch.bfloat16)
+        assert np.isfinite(np64(pp.grad)).all()
