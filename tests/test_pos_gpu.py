@@ -122,3 +122,64 @@ def test_pos_against_oracle_c5_shape(cuda_device):
         dP = (dq + dk).sum(axis=0, keepdims=True)
         check(f"pos C5 dP h{h}", pp.grad[:, h:h + 1], dP, torch.bfloat16)
         assert np.isfinite(np64(pp.grad)).all()
+
+
+@pytest.mark.parametrize(
+    "B,H,N,D,dtype,softmax,shared,causal,npre",
+    [
+        (2, 3, 700, 64, torch.bfloat16, True, True, True, 0),  # N > 576
+        (2, 2, 300, 128, torch.bfloat16, True, False, True, 0),  # D = 128 (paired dK/dV kernel)
+        (2, 2, 260, 32, torch.bfloat16, False, True, True, 0),  # D = 32, non-softmax
+        (1, 3, 700, 64, torch.float16, True, True, False, 0),  # fp16, not causal
+        (2, 2, 650, 64, torch.bfloat16, True, False, True, 4),  # register tokens seen by every query
+        (2, 2, 150, 64, torch.float32, True, True, True, 0),  # fp32
+        (2, 2, 150, 96, torch.float32, False, False, True, 0),  # fp32, D = 96 padded to 128
+    ],
+)
+def test_pos_streaming_against_oracle(cuda_device, B, H, N, D, dtype, softmax, shared, causal, npre):
+    """Shapes outside the head-resident kernels: the op adds the term (q + P,
+    k + P, each sum rounded to the element type) and runs the streaming
+    kernels; autograd forms the term's gradient.  O, dQ, dK, dV against the
+    float64 oracle evaluated on those rounded sums, to the parity tests'
+    bounds (and, for 16-bit types, within the rounding model's ratio), and the
+    term's gradient against the oracle's sum_b (dq + dk) (dq + dk per batch
+    entry for a per-batch term)."""
+    import numpy as np
+
+    from oracle import rbf_oracle as ro
+    from test_parity_gpu import check, np64
+
+    gamma = 1.0 / (2 * math.sqrt(D))
+    q, k, v, do, P = inputs(B, H, N, D, dtype, cuda_device, seed=N + D + B, shared=shared)
+    a = _lib.Args()
+    a.abi_version, a.variant, a.dtype = _lib.ABI_VERSION, 0 if softmax else 1, _lib.DTYPE_CODES[dtype]
+    a.B, a.H, a.N, a.D, a.causal, a.gamma = B, H, N, D, int(causal), gamma
+    assert not _lib.pos_supported(a)
+    fn = ra.run_triton_rbf if softmax else ra.run_triton_non_softmax_rbf
+    qq, kk, vv, pp = (x.clone().requires_grad_(True) for x in (q, k, v, P))
+    out = fn(qq, kk, vv, causal, sm_scale=gamma, num_prefix=npre, pos=pp)
+    out.backward(do)
+    torch.cuda.synchronize()
+    qs, ks = q + P, k + P  # rounded to the element type, as separate adds store them
+    fwd = ro.softmax_forward if softmax else ro.non_softmax_forward
+    bwd = ro.softmax_backward if softmax else ro.non_softmax_backward
+    r = ro.rounder("bf16" if dtype == torch.bfloat16 else "fp16") if dtype != torch.float32 else None
+    name0 = f"pos stream {str(dtype)[6:]} N{N} D{D} {'sm' if softmax else 'ns'}{'' if causal else ' nc'} p{npre}"
+    for b in range(B):
+        for h in range(H):
+            sl = (slice(b, b + 1), slice(h, h + 1))
+            arr = [np64(x)[sl] for x in (qs, ks, v, do)]
+            O = fwd(arr[0], arr[1], arr[2], gamma, causal, npre)
+            O = O[0] if softmax else O
+            grads = bwd(*arr, gamma, causal, npre)
+            model = (ro.rounded_model(*arr, gamma, softmax=softmax, causal=causal, num_prefix=npre, rnd=r, out_rnd=r)
+                     if r is not None else [None] * 4)
+            for i, (name, got, ref) in enumerate(zip(("O", "dQ", "dK", "dV"), (out, qq.grad, kk.grad, vv.grad),
+                                                     (O,) + tuple(grads))):
+                check(f"{name0} b{b}h{h} {name}", got[sl], ref, dtype, kind=name, model=model[i])
+    for h in range(H):
+        arr = [np64(x)[:, h:h + 1] for x in (qs, ks, v, do)]
+        dq, dk, _ = bwd(*arr, gamma, causal, npre)
+        dP = (dq + dk).sum(axis=0, keepdims=True) if shared else dq + dk
+        check(f"{name0} dP h{h}", pp.grad[:, h:h + 1], dP, dtype)
+    assert np.isfinite(np64(pp.grad)).all()
