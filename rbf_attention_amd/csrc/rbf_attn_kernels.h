@@ -559,6 +559,165 @@ struct TileLayout {
   }
 };
 
+// ---------------------------------------------------------------------------
+// LDS-DMA staging of chunk-major tiles (16-bit elements, 128 features).
+//
+// global_load_lds_dwordx4 writes each lane's 16 bytes to consecutive 16-byte
+// LDS slots (M0 base + 16 * lane), i.e. 1 KB per instruction: in a CLayout
+// tile, 64 consecutive rows of one chunk column.  So one instruction stages
+// rows r0 .. r0 + 63 of chunk ch, lane l reading row r0 + l, and no register
+// ever holds the tile.  Rows outside [0, N) read row 0 or N - 1 instead: the
+// kernels mask such keys and queries by their -inf norm or offset, never by
+// their values, which only have to be finite.
+//
+// A pipeline of three tiles (dma_pipeline) runs the compute of tile t while
+// tile t + 1 is landed in LDS (its per-row terms formed from LDS) and tile
+// t + 2 is in flight.  One barrier per tile: before it every wave waits for
+// its own DMA of tile t + 1 (issued a whole tile earlier); after it tile
+// t + 1 and the per-row terms of tile t (formed during tile t - 1) are
+// visible to every wave.
+//
+// The DMA instruction is issued from inline assembly, so the compiler neither
+// tracks it nor waits for it: every wait for it is the explicit one before
+// the barrier.  (The compiler's own waits for its loads stay correct, since
+// vector-memory operations retire in order; at worst they also wait for a
+// DMA issued earlier.  Through the compiler builtin, the DMA made every read
+// of the tiles wait for the DMA in flight unless the three buffers were
+// separate arrays in an unrolled loop, which cost the kernels spills.)
+// ---------------------------------------------------------------------------
+// s_waitcnt vmcnt(0): this wave's vector-memory loads (LDS-DMA included) done.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Work-group barrier for LDS data only: this wave's LDS operations complete,
+// then s_barrier; the compiler moves no memory access across it.
+// __syncthreads() also waits for every outstanding vector-memory load (its
+// fence), which would make a mid-tile barrier wait for the DMA in flight.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource over `bytes` bytes from `base` (stride 0, gfx9 data
+// format word): a load at byte offset >= bytes -- a negative offset included,
+// read as unsigned -- returns zeros.
+__device__ __forceinline__ i32x4_t buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  i32x4_t r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+  r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+  r.w = 0x00020000;
+  return r;
+}
+
+// buffer_load_dwordx4 ... lds: 16 bytes per lane from byte offset voff of
+// the buffer to LDS byte address lds + 16 * lane (lds wave-uniform).  M0
+// carries the LDS address; nothing else in these kernels uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(uint32_t voff, i32x4_t rsrc, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rsrc), "s"(lds)
+               : "memory", "m0");
+}
+// The same with 4 bytes per lane (LDS address lds + 4 * lane).
+__device__ __forceinline__ void dma4(uint32_t voff, i32x4_t rsrc, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds" : : "v"(voff), "s"(rsrc), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// LDS byte address of a __shared__ element.
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(const T* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) T*)p;
+}
+
+// The DMA of two (ROWS x 128) chunk-major tiles -- tokens tok0 .. tok0 +
+// ROWS - 1 of slices A and B, each (N, 128) with row stride sa / sb -- by W
+// waves: 2 * (ROWS / 64) * 16 instructions of 64 rows x one chunk, dealt
+// round-robin to the waves.  A wave's lane offsets (relative to the tile's
+// first row) and LDS offsets are fixed, so a tile costs one add per
+// instruction.  Tokens outside [0, N) read zeros (buffer range check; the
+// host keeps N * stride * sizeof(T) below 2^31).
+template <typename T, int ROWS, int W>
+struct DmaPair {
+  static_assert(sizeof(T) == 2 && ROWS % 64 == 0, "DMA tiles: 16-bit, whole 64-row groups");
+  static constexpr int PER = (ROWS / 64) * 16, NI = 2 * PER, NIW = NI / W;
+  static_assert(NI % W == 0, "every wave issues the same number of DMA instructions");
+  i32x4_t ra, rb;
+  uint32_t voff[NIW];  // lane byte offset of instruction j, tile row 0 at offset 0
+  int loff[NIW];       // element offset of instruction j's 1 KB in its tile
+  int rowa, rowb;      // row strides in bytes
+  int wave;
+
+  __device__ inline void init(const T* A, int64_t sa, const T* B, int64_t sb, int N, int wave_, int lane) {
+    wave = wave_;
+    rowa = (int)(sa * (int64_t)sizeof(T));
+    rowb = (int)(sb * (int64_t)sizeof(T));
+    ra = buffer_rsrc(A, (uint32_t)N * (uint32_t)rowa);
+    rb = buffer_rsrc(B, (uint32_t)N * (uint32_t)rowb);
+#pragma unroll
+    for (int j = 0; j < NIW; ++j) {
+      const int i = wave + j * W, k = i % PER, rg = k / 16, ch = k % 16;
+      const int row = i < PER ? rowa : rowb;
+      voff[j] = (uint32_t)((64 * rg + lane) * row + 16 * ch);
+      loff[j] = CLayout<ROWS>::off(64 * rg, 8 * ch);
+    }
+  }
+
+  __device__ inline void issue(int tok0, T* tA, T* tB) const {
+    const uint32_t la = lds_addr(tA), lb = lds_addr(tB);
+#pragma unroll
+    for (int j = 0; j < NIW; ++j) {
+      // instruction wave + j * W reads slice A when below PER (known per j
+      // when W divides PER)
+      const bool isa = PER % W == 0 ? j < PER / W : wave + j * W < PER;
+      if (isa) dma16(voff[j] + (uint32_t)(tok0 * rowa), ra, la + 2u * (uint32_t)loff[j]);
+      else dma16(voff[j] + (uint32_t)(tok0 * rowb), rb, lb + 2u * (uint32_t)loff[j]);
+    }
+  }
+};
+
+// nrm[row] = -0.5 ||row||^2 (fp32, from the element-type values) of a landed
+// (ROWS x 128) chunk-major tile, -inf for tokens outside [0, N).  NT / ROWS
+// consecutive threads share a row.
+template <typename T, int ROWS, int NT>
+__device__ __forceinline__ void tile_neg_halfnorms(const T* tile, float* nrm, int tok0, int N, int tid) {
+  constexpr int TPR = NT / ROWS, CPT = 16 / TPR;
+  static_assert(NT % ROWS == 0 && TPR <= 16 && 16 % TPR == 0, "threads per row must divide 16");
+  const int row = tid / TPR, part = tid % TPR;
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) s += sumsq8<T>(ld8<T>(tile + CLayout<ROWS>::off(row, 8 * (part * CPT + j))));
+  s = group_sum<TPR>(s);
+  const int tok = tok0 + row;
+  if (part == 0) nrm[row] = (tok >= 0 && tok < N) ? -0.5f * s : -__builtin_inff();
+}
+
+// The three-tile pipeline.  issue(t, b) requests tile t into buffer b,
+// land(t, b) forms tile t's per-row terms from buffer b (after its data is
+// visible), compute(t, b) runs tile t from buffer b (b = t mod 3).
+template <typename Issue, typename Land, typename Compute>
+__device__ __forceinline__ void dma_pipeline(int nt, Issue&& issue, Land&& land, Compute&& compute) {
+  if (nt <= 0) return;
+  issue(0, 0);
+  if (nt > 1) issue(1, 1);
+  wait_vmem();
+  __syncthreads();
+  land(0, 0);
+  int b0 = 0, b1 = 1, b2 = 2;  // buffers of tiles t, t + 1, t + 2
+  for (int t = 0; t < nt; ++t) {
+    wait_vmem();
+    lds_barrier();
+    if (t + 2 < nt) issue(t + 2, b2);
+    if (t + 1 < nt) land(t + 1, b1);
+    compute(t, b0);
+    const int b = b0;
+    b0 = b1;
+    b1 = b2;
+    b2 = b;
+  }
+}
+
 // Work-group -> (b*H + h, bin).  The hardware deals work-groups round-robin
 // over the 8 XCDs (block id mod 8) and each XCD starts its share in block-id
 // order.  When B*H is a multiple of 8, XCD x owns whole heads
@@ -729,7 +888,9 @@ __device__ inline typename Elem<T>::frag ones_row_frag(int n) {
 constexpr float kBoundMargin = 60.f;  // P <= 2^60 under the static bound
 constexpr float kSumLow = 0x1p-60f, kSumHigh = 0x1p100f;
 
-template <typename T, int DP, int W, int BN, bool SOFTMAX>
+// DMA: K and V tiles staged by LDS-DMA (dma_pipeline; 16-bit, D = 128 only)
+// instead of through registers.
+template <typename T, int DP, int W, int BN, bool SOFTMAX, bool DMA = false>
 __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -740,11 +901,19 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
   // of V.
   constexpr bool TR = sizeof(T) == 2;
   typedef TileLayout<T, BN, DP> TLy;
+  static_assert(!DMA || (TR && TLy::CM), "LDS-DMA staging is for chunk-major 16-bit tiles");
   constexpr int TSZ = TLy::SIZE;
-  __shared__ __attribute__((aligned(16))) T sK[2][TSZ];
-  __shared__ __attribute__((aligned(16))) T sVt[2][TR ? TSZ : DP * LDT];
+  // register staging: two buffers each (a single element when DMA)
+  constexpr int NB2 = DMA ? 1 : 2;
+  __shared__ __attribute__((aligned(16))) T sK[NB2][DMA ? 8 : TSZ];
+  __shared__ __attribute__((aligned(16))) T sVt[NB2][DMA ? 8 : (TR ? TSZ : DP * LDT)];
   auto roff = [](int row, int col) { return TLy::off(row, col); };
-  __shared__ __attribute__((aligned(16))) float sKn[2][BN];
+  __shared__ __attribute__((aligned(16))) float sKn[NB2][DMA ? 1 : BN];
+  // LDS-DMA staging: three buffers each (a single element without DMA)
+  constexpr int NB3 = DMA ? 3 : 1;
+  __shared__ __attribute__((aligned(16))) T dK[NB3][DMA ? TSZ : 8];
+  __shared__ __attribute__((aligned(16))) T dV[NB3][DMA ? TSZ : 8];
+  __shared__ __attribute__((aligned(16))) float dN[NB3][DMA ? BN : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -804,20 +973,10 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
     lacc = zero16();
     lrow = 0.f;
     m_run = !SOFTMAX ? qn2 : (SAFE ? -__builtin_inff() : qn2 - kBoundMargin);
-    load_kv(0);
-    for (int kt = 0; kt < nkt; ++kt) {
-      const int buf = kt & 1;
-      if constexpr (TR) {
-        TLy::store(tk, sK[buf], tid);
-        TLy::store(tv, sVt[buf], tid);
-      } else {
-        tk.template store_rows<LDR>(sK[buf], tid);
-        tv.template store_trans<LDT>(sVt[buf], tid);
-      }
-      tk.store_neg_halfnorm(sKn[buf], tid);
-      __syncthreads();
-      if (kt + 1 < nkt) load_kv(kt + 1);
-      if (!wave_on) continue;
+    // The blocks of key tile kt against this wave's queries, from tiles kbuf
+    // (K), vbuf (V, or V^T for fp32) and norms nbuf.
+    auto tile = [&](int kt, const T* kbuf, const T* vbuf, const float* nbuf) {
+      if (!wave_on) return;
       const int kblk0 = kt * KB - kshift;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
@@ -825,8 +984,8 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
         if (!blk_any(q0, k0, causal, npre)) continue;
         frag kA[KS];
 #pragma unroll
-        for (int t = 0; t < KS; ++t) kA[t] = ld8<T>(sK[buf] + roff(32 * kb + n, 16 * t + 8 * h));
-        f32x16_t s = ld_rows16(sKn[buf] + 32 * kb, h);
+        for (int t = 0; t < KS; ++t) kA[t] = ld8<T>(kbuf + roff(32 * kb + n, 16 * t + 8 * h));
+        f32x16_t s = ld_rows16(nbuf + 32 * kb, h);
 #pragma unroll
         for (int t = 0; t < KS; ++t) s = E::mma(kA[t], qf[t], s);
         // V^T fragments are read while the S MFMAs and the softmax run.
@@ -835,8 +994,8 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
         for (int d = 0; d < ND; ++d)
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            if constexpr (TR) vA[d][t] = TLy::tr(sVt[buf], 32 * kb + 16 * t, 32 * d, lane);
-            else vA[d][t] = ld8<T>(sVt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h));
+            if constexpr (TR) vA[d][t] = TLy::tr(vbuf, 32 * kb + 16 * t, 32 * d, lane);
+            else vA[d][t] = ld8<T>(vbuf + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h));
           }
         if (!blk_nomask(q0, k0, causal, npre)) mask_key_rows(s, k0, h, jmax);
         if constexpr (SOFTMAX && SAFE) {
@@ -866,6 +1025,31 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
           for (int d = 0; d < ND; ++d) oacc[d] = E::mma(vA[d][t], pf[t], oacc[d]);
           if constexpr (SOFTMAX) lacc = E::mma(onesA, pf[t], lacc);
         }
+      }
+    };
+    if constexpr (DMA) {
+      auto tok0_of = [&](int kt) { return org + 32 * (kt * KB - kshift); };
+      DmaPair<T, BN, W> dma;
+      dma.init(K, p.sk[2], V, p.sv[2], N, wave, lane);
+      dma_pipeline(
+          nkt, [&](int kt, int b) { dma.issue(tok0_of(kt), dK[b], dV[b]); },
+          [&](int kt, int b) { tile_neg_halfnorms<T, BN, NT>(dK[b], dN[b], tok0_of(kt), N, tid); },
+          [&](int kt, int b) { tile(kt, dK[b], dV[b], dN[b]); });
+    } else {
+      load_kv(0);
+      for (int kt = 0; kt < nkt; ++kt) {
+        const int buf = kt & 1;
+        if constexpr (TR) {
+          TLy::store(tk, sK[buf], tid);
+          TLy::store(tv, sVt[buf], tid);
+        } else {
+          tk.template store_rows<LDR>(sK[buf], tid);
+          tv.template store_trans<LDT>(sVt[buf], tid);
+        }
+        tk.store_neg_halfnorm(sKn[buf], tid);
+        __syncthreads();
+        if (kt + 1 < nkt) load_kv(kt + 1);
+        tile(kt, sK[buf], sVt[buf], sKn[buf]);
       }
     }
   };
@@ -911,10 +1095,10 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
 // 512 / WPE): the binned 16-bit D <= 64 forward keeps three, as it has
 // without the bin loop around its body.
 template <typename T, int DP, int W, int BN, bool SOFTMAX, bool BIN = false,
-          int WPE = (BIN && sizeof(T) == 2 && DP <= 64) ? 3 : 1>
+          int WPE = (BIN && sizeof(T) == 2 && DP <= 64) ? 3 : 1, bool DMA = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void rbf_fwd_kernel(const Params p) {
   for_each_group<BIN>(p, (p.nblk + W - 1) / W, p.causal != 0,
-                 [&](int bh, int grp) { rbf_fwd_group<T, DP, W, BN, SOFTMAX>(p, bh, grp); });
+                 [&](int bh, int grp) { rbf_fwd_group<T, DP, W, BN, SOFTMAX, DMA>(p, bh, grp); });
 }
 
 // ---------------------------------------------------------------------------
@@ -926,7 +1110,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) v
 //   S^T = K Q^T (init -0.5||k||^2), P = exp2(c S^T - L),
 //   dP^T = V dO^T (init -Delta), dS = P dP^T, dQ^T += K^T dS^T.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX, bool EARLY = true>
+// DMA: K and V tiles staged by LDS-DMA (dma_pipeline; 16-bit, D = 128 only)
+// instead of through registers.
+template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX, bool EARLY = true, bool DMA = false>
 __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int grp) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -936,12 +1122,20 @@ __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int gr
   // reads; fp32 stages a transposed copy.
   constexpr bool TR = sizeof(T) == 2;
   typedef TileLayout<T, BN, DP> TLy;
+  static_assert(!DMA || (TR && TLy::CM), "LDS-DMA staging is for chunk-major 16-bit tiles");
   constexpr int TSZ = TLy::SIZE;
-  __shared__ __attribute__((aligned(16))) T sK[2][TSZ];
+  // register staging: two buffers each (a single element when DMA)
+  constexpr int NB2 = DMA ? 1 : 2;
+  __shared__ __attribute__((aligned(16))) T sK[NB2][DMA ? 8 : TSZ];
   __shared__ __attribute__((aligned(16))) T sKt[TR ? 1 : 2][TR ? 8 : DP * LDT];
-  __shared__ __attribute__((aligned(16))) T sV[2][TSZ];
+  __shared__ __attribute__((aligned(16))) T sV[NB2][DMA ? 8 : TSZ];
   auto roff = [](int row, int col) { return TLy::off(row, col); };
-  __shared__ __attribute__((aligned(16))) float sKn[2][BN];
+  __shared__ __attribute__((aligned(16))) float sKn[NB2][DMA ? 1 : BN];
+  // LDS-DMA staging: three buffers each (a single element without DMA)
+  constexpr int NB3 = DMA ? 3 : 1;
+  __shared__ __attribute__((aligned(16))) T dK[NB3][DMA ? TSZ : 8];
+  __shared__ __attribute__((aligned(16))) T dV[NB3][DMA ? TSZ : 8];
+  __shared__ __attribute__((aligned(16))) float dN[NB3][DMA ? BN : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1018,30 +1212,10 @@ __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int gr
     rsum[j] = 0.f;
   }
 
-  TileFor<T, BN, DP, NT> tk, tv;
-  {
-    const int tok0 = org + 32 * (-kshift);
-    tk.load(K, p.sk[2], tok0, N, D, tid);
-    tv.load(V, p.sv[2], tok0, N, D, tid);
-  }
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
-    if constexpr (TR) {
-      TLy::store(tk, sK[buf], tid);
-      TLy::store(tv, sV[buf], tid);
-    } else {
-      tk.template store_rows<LDR>(sK[buf], tid);
-      tk.template store_trans<LDT>(sKt[buf], tid);
-      tv.template store_rows<LDR>(sV[buf], tid);
-    }
-    tk.store_neg_halfnorm(sKn[buf], tid);
-    __syncthreads();
-    if (kt + 1 < nkt) {
-      const int tok1 = org + 32 * ((kt + 1) * KB - kshift);
-      tk.load(K, p.sk[2], tok1, N, D, tid);
-      tv.load(V, p.sv[2], tok1, N, D, tid);
-    }
-    if (!wave_on) continue;
+  // The blocks of key tile kt against this wave's queries, from tiles kbuf
+  // (K), ktbuf (K^T, fp32 only), vbuf (V) and norms nbuf.
+  auto tile = [&](int kt, const T* kbuf, const T* ktbuf, const T* vbuf, const float* nbuf) {
+    if (!wave_on) return;
     const int kblk0 = kt * KB - kshift;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
@@ -1057,10 +1231,10 @@ __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int gr
       frag kA[KS], vA[KS];
 #pragma unroll
       for (int t = 0; t < KS; ++t) {
-        kA[t] = ld8<T>(sK[buf] + roff(32 * kb + n, 16 * t + 8 * h));
-        vA[t] = ld8<T>(sV[buf] + roff(32 * kb + n, 16 * t + 8 * h));
+        kA[t] = ld8<T>(kbuf + roff(32 * kb + n, 16 * t + 8 * h));
+        vA[t] = ld8<T>(vbuf + roff(32 * kb + n, 16 * t + 8 * h));
       }
-      const f32x16_t kinit = ld_rows16(sKn[buf] + 32 * kb, h);
+      const f32x16_t kinit = ld_rows16(nbuf + 32 * kb, h);
       f32x16_t sacc[QPW], dpacc[QPW];
 #pragma unroll
       for (int j = 0; j < QPW; ++j) {
@@ -1081,8 +1255,8 @@ __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int gr
         for (int d = 0; d < ND; ++d)
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            if constexpr (TR) ktA[d][t] = TLy::tr(sK[buf], 32 * kb + 16 * t, 32 * d, lane);
-            else ktA[d][t] = ld8<T>(sKt[buf] + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h));
+            if constexpr (TR) ktA[d][t] = TLy::tr(kbuf, 32 * kb + 16 * t, 32 * d, lane);
+            else ktA[d][t] = ld8<T>(ktbuf + (32 * d + n) * LDT + tchunk<BN>(32 * d + n, 32 * kb + 16 * t + 8 * h));
           }
       };
       if constexpr (EARLY) read_kt();
@@ -1109,6 +1283,38 @@ __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int gr
 #pragma unroll
           for (int j = 0; j < QPW; ++j)
             if (act[j]) dqacc[j][d] = E::mma(ktA[d][t], sf[j][t], dqacc[j][d]);
+    }
+  };
+
+  auto tok0_of = [&](int kt) { return org + 32 * (kt * KB - kshift); };
+  if constexpr (DMA) {
+    DmaPair<T, BN, W> dma;
+    dma.init(K, p.sk[2], V, p.sv[2], N, wave, lane);
+    dma_pipeline(
+        nkt, [&](int kt, int b) { dma.issue(tok0_of(kt), dK[b], dV[b]); },
+        [&](int kt, int b) { tile_neg_halfnorms<T, BN, NT>(dK[b], dN[b], tok0_of(kt), N, tid); },
+        [&](int kt, int b) { tile(kt, dK[b], nullptr, dV[b], dN[b]); });
+  } else {
+    TileFor<T, BN, DP, NT> tk, tv;
+    tk.load(K, p.sk[2], tok0_of(0), N, D, tid);
+    tv.load(V, p.sv[2], tok0_of(0), N, D, tid);
+    for (int kt = 0; kt < nkt; ++kt) {
+      const int buf = kt & 1;
+      if constexpr (TR) {
+        TLy::store(tk, sK[buf], tid);
+        TLy::store(tv, sV[buf], tid);
+      } else {
+        tk.template store_rows<LDR>(sK[buf], tid);
+        tk.template store_trans<LDT>(sKt[buf], tid);
+        tv.template store_rows<LDR>(sV[buf], tid);
+      }
+      tk.store_neg_halfnorm(sKn[buf], tid);
+      __syncthreads();
+      if (kt + 1 < nkt) {
+        tk.load(K, p.sk[2], tok0_of(kt + 1), N, D, tid);
+        tv.load(V, p.sv[2], tok0_of(kt + 1), N, D, tid);
+      }
+      tile(kt, sK[buf], sKt[TR ? 0 : buf], sV[buf], sKn[buf]);
     }
   }
 
@@ -1143,10 +1349,11 @@ __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int gr
   }
 }
 
-template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX, bool EARLY = true, bool BIN = false>
+template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX, bool EARLY = true, bool BIN = false,
+          bool DMA = false>
 __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
   for_each_group<BIN>(p, (p.nblk + W * QPW - 1) / (W * QPW), p.causal != 0,
-                 [&](int bh, int grp) { rbf_bwd_dq_group<T, DP, W, QPW, BN, SOFTMAX, EARLY>(p, bh, grp); });
+                 [&](int bh, int grp) { rbf_bwd_dq_group<T, DP, W, QPW, BN, SOFTMAX, EARLY, DMA>(p, bh, grp); });
 }
 
 // ---------------------------------------------------------------------------
@@ -1479,17 +1686,28 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
 // reads before its MFMAs (sched_group_barrier), trading registers for hidden
 // LDS latency.
 // ---------------------------------------------------------------------------
-template <typename T, int DP, int NP, int BM, bool SOFTMAX, bool SGB = false>
+// DMA: Q and dO tiles staged by LDS-DMA (dma_pipeline; D = 128 only), the
+// per-query offsets through two registers of the first wave.
+template <typename T, int DP, int NP, int BM, bool SOFTMAX, bool SGB = false, bool DMA = false>
 __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh, int grp) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   static_assert(sizeof(T) == 2, "the paired kernel reads transposed operands with ds_read_b64_tr_b16");
   constexpr int W = 2 * NP, NT = 64 * W, QB = BM / 32, KS = DP / 16, ND = DP / 32;
   typedef TileLayout<T, BM, DP> TLy;
-  __shared__ __attribute__((aligned(16))) T sQ[2][TLy::SIZE];
-  __shared__ __attribute__((aligned(16))) T sD[2][TLy::SIZE];
-  __shared__ __attribute__((aligned(16))) float sOff[2][BM];
-  __shared__ __attribute__((aligned(16))) float sDel[2][BM];
+  static_assert(!DMA || TLy::CM, "LDS-DMA staging is for chunk-major tiles");
+  // register staging: two buffers each; LDS-DMA staging: three (the other
+  // form's arrays shrink to a single element)
+  constexpr int NB2 = DMA ? 1 : 2, NB3 = DMA ? 3 : 1;
+  __shared__ __attribute__((aligned(16))) T sQ[NB2][DMA ? 8 : TLy::SIZE];
+  __shared__ __attribute__((aligned(16))) T sD[NB2][DMA ? 8 : TLy::SIZE];
+  __shared__ __attribute__((aligned(16))) float sOff[NB2][DMA ? 1 : BM];
+  __shared__ __attribute__((aligned(16))) float sDel[NB2][DMA ? 1 : BM];
+  __shared__ __attribute__((aligned(16))) T dQt[NB3][DMA ? TLy::SIZE : 8];
+  __shared__ __attribute__((aligned(16))) T dDt[NB3][DMA ? TLy::SIZE : 8];
+  __shared__ __attribute__((aligned(16))) float dOff[NB3][DMA ? BM : 1];
+  __shared__ __attribute__((aligned(16))) float dDel[NB3][DMA ? BM : 1];
+  __shared__ __attribute__((aligned(16))) float dRaw[NB3][2][DMA ? BM : 1];  // L, Delta as loaded
   __shared__ __attribute__((aligned(16))) f32x4_t sP[NP][QB][4][64];
 
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
@@ -1561,17 +1779,9 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
   // role on its own.
   auto tile_loop = [&](auto role) {
     constexpr bool PW = decltype(role)::value;
-    load_tile(qt_lo);
-    for (int qt = qt_lo; qt < nqt_all; ++qt) {
-      const int buf = qt & 1;
-      TLy::store(tq, sQ[buf], tid);
-      TLy::store(td, sD[buf], tid);
-      if (tid < BM) {
-        sOff[buf][tid] = offr;
-        sDel[buf][tid] = delr;
-      }
-      __syncthreads();
-      if (qt + 1 < nqt_all) load_tile(qt + 1);
+    // Query tile qt from tiles sQb (Q), sDb (dO) and per-query terms offb
+    // (-L/c), delb (-Delta); the mid-tile barrier hands P to the dS-waves.
+    auto compute = [&](int qt, const T* sQb, const T* sDb, const float* offb, const float* delb) {
       const int qblk0 = qt * QB - qshift;
       bool act[QB];
 #pragma unroll
@@ -1583,9 +1793,9 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
         for (int qb = 0; qb < QB; ++qb) {
           if (!act[qb]) continue;
           const int q0 = org + 32 * (qblk0 + qb);
-          f32x16_t s = ld_rows16(sOff[buf] + 32 * qb, h);
+          f32x16_t s = ld_rows16(offb + 32 * qb, h);
 #pragma unroll
-          for (int t = 0; t < KS; ++t) s = E::mma(ld8<T>(sQ[buf] + TLy::off(32 * qb + n, 16 * t + 8 * h)), kv[t], s);
+          for (int t = 0; t < KS; ++t) s = E::mma(ld8<T>(sQb + TLy::off(32 * qb + n, 16 * t + 8 * h)), kv[t], s);
           if constexpr (SGB) {
             __builtin_amdgcn_sched_group_barrier(0x100, KS + 4, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, KS, 0);
@@ -1601,7 +1811,8 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
 #pragma unroll
           for (int u = 0; u < 4; ++u) sP[j][qb][u][lane] = pv[u];
         }
-        __syncthreads();
+        if constexpr (DMA) lds_barrier();
+        else __syncthreads();
         // phase 2: dV^T += dO^T P
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
@@ -1610,7 +1821,7 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
           for (int d = 0; d < ND; ++d)
 #pragma unroll
             for (int t = 0; t < 2; ++t)
-              acc[d] = E::mma(TLy::tr(sD[buf], 32 * qb + 16 * t, 32 * d, lane), pf[qb][t], acc[d]);
+              acc[d] = E::mma(TLy::tr(sDb, 32 * qb + 16 * t, 32 * d, lane), pf[qb][t], acc[d]);
           if constexpr (SGB) {
             __builtin_amdgcn_sched_group_barrier(0x100, 4 * ND, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 2 * ND, 0);
@@ -1623,17 +1834,18 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
         for (int qb = 0; qb < QB; ++qb) {
           if (!act[qb]) continue;
           f32x16_t dp;
-          if constexpr (SOFTMAX) dp = ld_rows16(sDel[buf] + 32 * qb, h);
+          if constexpr (SOFTMAX) dp = ld_rows16(delb + 32 * qb, h);
           else dp = zero16();
 #pragma unroll
-          for (int t = 0; t < KS; ++t) dp = E::mma(ld8<T>(sD[buf] + TLy::off(32 * qb + n, 16 * t + 8 * h)), kv[t], dp);
+          for (int t = 0; t < KS; ++t) dp = E::mma(ld8<T>(sDb + TLy::off(32 * qb + n, 16 * t + 8 * h)), kv[t], dp);
           dpacc[qb] = dp;
           if constexpr (SGB) {
             __builtin_amdgcn_sched_group_barrier(0x100, KS + (SOFTMAX ? 4 : 0), 0);
             __builtin_amdgcn_sched_group_barrier(0x008, KS, 0);
           }
         }
-        __syncthreads();
+        if constexpr (DMA) lds_barrier();
+        else __syncthreads();
         // phase 2: dS = P dP, dK^T += Q^T dS
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
@@ -1653,12 +1865,56 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
           for (int d = 0; d < ND; ++d)
 #pragma unroll
             for (int t = 0; t < 2; ++t)
-              acc[d] = E::mma(TLy::tr(sQ[buf], 32 * qb + 16 * t, 32 * d, lane), sf[t], acc[d]);
+              acc[d] = E::mma(TLy::tr(sQb, 32 * qb + 16 * t, 32 * d, lane), sf[t], acc[d]);
           if constexpr (SGB) {
             __builtin_amdgcn_sched_group_barrier(0x100, 4 * ND, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 2 * ND, 0);
           }
         }
+      }
+    };
+    if constexpr (DMA) {
+      static_assert(!DMA || BM == 64, "one 64-lane DMA per per-query term");
+      // The tile's raw L and Delta are DMA'd with it (the last wave issues
+      // them) and turned into -L/c and -Delta by the first wave once landed.
+      DmaPair<T, BM, W> dma;
+      dma.init(Q, p.sq[2], dO, p.sdo[2], N, wave, lane);
+      const i32x4_t roff = buffer_rsrc(offg, 4u * (uint32_t)N);
+      const i32x4_t rdel = buffer_rsrc(SOFTMAX ? delg : offg, 4u * (uint32_t)N);
+      auto tok0_of = [&](int qt) { return org + 32 * (qt * QB - qshift); };
+      dma_pipeline(
+          nqt_all - qt_lo,
+          [&](int t, int b) {
+            const int tok0 = tok0_of(qt_lo + t);
+            dma.issue(tok0, dQt[b], dDt[b]);
+            if (wave == W - 1) {
+              const uint32_t vo = 4u * (uint32_t)(tok0 + lane);  // negative tokens: out of range
+              dma4(vo, roff, lds_addr(dRaw[b][0]));
+              if constexpr (SOFTMAX) dma4(vo, rdel, lds_addr(dRaw[b][1]));
+            }
+          },
+          [&](int t, int b) {
+            if (tid < BM) {
+              const int tok = tok0_of(qt_lo + t) + tid;
+              const bool ok = tok >= 0 && tok < N;
+              dOff[b][tid] = ok ? -dRaw[b][0][tid] * inv_c : -__builtin_inff();  // padding queries: P = 0
+              dDel[b][tid] = (SOFTMAX && ok) ? -dRaw[b][1][tid] : 0.f;
+            }
+          },
+          [&](int t, int b) { compute(qt_lo + t, dQt[b], dDt[b], dOff[b], dDel[b]); });
+    } else {
+      load_tile(qt_lo);
+      for (int qt = qt_lo; qt < nqt_all; ++qt) {
+        const int buf = qt & 1;
+        TLy::store(tq, sQ[buf], tid);
+        TLy::store(td, sD[buf], tid);
+        if (tid < BM) {
+          sOff[buf][tid] = offr;
+          sDel[buf][tid] = delr;
+        }
+        __syncthreads();
+        if (qt + 1 < nqt_all) load_tile(qt + 1);
+        compute(qt, sQ[buf], sD[buf], sOff[buf], sDel[buf]);
       }
     }
   };
@@ -1693,10 +1949,10 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
     }
 }
 
-template <typename T, int DP, int NP, int BM, bool SOFTMAX, bool SGB = false, bool BIN = false>
+template <typename T, int DP, int NP, int BM, bool SOFTMAX, bool SGB = false, bool BIN = false, bool DMA = false>
 __global__ __launch_bounds__(128 * NP) void rbf_bwd_dkdv_pair_kernel(const Params p) {
   for_each_group<BIN>(p, (p.nblk + NP - 1) / NP, false,
-                 [&](int bh, int grp) { rbf_bwd_dkdv_pair_group<T, DP, NP, BM, SOFTMAX, SGB>(p, bh, grp); });
+                 [&](int bh, int grp) { rbf_bwd_dkdv_pair_group<T, DP, NP, BM, SOFTMAX, SGB, DMA>(p, bh, grp); });
 }
 
 }  // namespace rbf

@@ -154,16 +154,27 @@ bool use_hr(const Params& p, int nb_max, int which) {
 }
 constexpr int kHrBlocks64 = kHrMaxBlocks;  // D <= 64: N <= 576
 
-template <int DP, bool SM, int W, int BN, bool BIN = false>
+// LDS-DMA tile staging (16-bit, D = 128: the streaming kernels' tiles go from
+// global memory straight into LDS, three tiles in flight).  The DMA reads
+// through buffer resources whose byte range (N rows of each slice) must stay
+// below 2^31.  RBF_ATTN_DMA=0 keeps the register-staged kernels.
+bool dma_fits(int64_t N, int64_t stride) { return N * stride * (int64_t)sizeof(Elt) < (int64_t(1) << 31); }
+bool use_dma(const Params& p) {
+  static const int forced = env_choice("RBF_ATTN_DMA");
+  return !kIsF32 && forced != 0 && p.D == 128 && dma_fits(p.N, p.sk[2]) && dma_fits(p.N, p.sv[2]) &&
+         dma_fits(p.N, p.sq[2]) && dma_fits(p.N, p.sdo[2]);
+}
+
+template <int DP, bool SM, int W, int BN, bool BIN = false, bool DMA = false>
 hipError_t fwd_cfg(const Params& p, hipStream_t st) {
-  auto k = rbf_fwd_kernel<Elt, DP, W, BN, SM, BIN>;
+  auto k = rbf_fwd_kernel<Elt, DP, W, BN, SM, BIN, (BIN && sizeof(Elt) == 2 && DP <= 64) ? 3 : 1, DMA>;
   static const int wgs = wgs_per_cu(k, 64 * W);
   return launch(k, p, W, 64 * W, wgs, BIN, st);
 }
 
-template <int DP, bool SM, int W, int QPW, int BN, bool EARLY = true, bool BIN = false>
+template <int DP, bool SM, int W, int QPW, int BN, bool EARLY = true, bool BIN = false, bool DMA = false>
 hipError_t dq_cfg(const Params& p, hipStream_t st) {
-  auto k = rbf_bwd_dq_kernel<Elt, DP, W, QPW, BN, SM, EARLY, BIN>;
+  auto k = rbf_bwd_dq_kernel<Elt, DP, W, QPW, BN, SM, EARLY, BIN, DMA>;
   static const int wgs = wgs_per_cu(k, 64 * W);
   return launch(k, p, W * QPW, 64 * W, wgs, BIN, st);
 }
@@ -176,9 +187,9 @@ hipError_t dkdv_cfg(const Params& p, hipStream_t st) {
   return launch(k, p, W * KPW, 64 * W, wgs, BIN, st);
 }
 
-template <int DP, bool SM, int NP, int BM, bool SGB = false, bool BIN = false>
+template <int DP, bool SM, int NP, int BM, bool SGB = false, bool BIN = false, bool DMA = false>
 hipError_t dkdv_pair_cfg(const Params& p, hipStream_t st) {
-  auto k = rbf_bwd_dkdv_pair_kernel<Elt, DP, NP, BM, SM, SGB, BIN>;
+  auto k = rbf_bwd_dkdv_pair_kernel<Elt, DP, NP, BM, SM, SGB, BIN, DMA>;
   static const int wgs = wgs_per_cu(k, 128 * NP);
   return launch(k, p, NP, 128 * NP, wgs, BIN, st);
 }
@@ -209,6 +220,7 @@ hipError_t fwd_default(const Params& p, hipStream_t st) {
     if (p.N >= kLongSeq) return bins_fit(p) ? fwd_cfg<DP, SM, 8, 128, true>(p, st) : fwd_cfg<DP, SM, 8, 128>(p, st);
     return bins_fit(p) ? fwd_cfg<DP, SM, 4, 64, true>(p, st) : fwd_cfg<DP, SM, 4, 64>(p, st);
   } else {
+    if (use_dma(p)) return bins_fit(p) ? fwd_cfg<DP, SM, 8, 64, true, true>(p, st) : fwd_cfg<DP, SM, 8, 64, false, true>(p, st);
     return bins_fit(p) ? fwd_cfg<DP, SM, 8, 64, true>(p, st) : fwd_cfg<DP, SM, 8, 64>(p, st);
   }
 }
@@ -227,8 +239,11 @@ hipError_t dq_default(const Params& p, hipStream_t st) {
   if constexpr (kIsF32) return dq_cfg<DP, SM, 4, 1, 32>(p, st);
   else if constexpr (DP <= 64)
     return bins_fit(p) ? dq_cfg<DP, SM, 4, 1, 128, true, true>(p, st) : dq_cfg<DP, SM, 4, 1, 128>(p, st);
-  else
+  else {
+    if (use_dma(p))
+      return bins_fit(p) ? dq_cfg<DP, SM, 8, 1, 64, true, true, true>(p, st) : dq_cfg<DP, SM, 8, 1, 64, true, false, true>(p, st);
     return bins_fit(p) ? dq_cfg<DP, SM, 8, 1, 32, true, true>(p, st) : dq_cfg<DP, SM, 8, 1, 32>(p, st);
+  }
 }
 
 template <int DP, bool SM>
@@ -250,7 +265,9 @@ hipError_t dkdv_default(const Params& p, hipStream_t st) {
                        : dkdv_cfg<DP, SM, 4, 1, 128, false>(p, st);
   } else {
     // the long-sequence paired kernel measured slower with the bin loop
-    if (p.N >= kLongSeq) return dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st);
+    // (LDS-DMA for long sequences only: the two-pair binned form spills with it)
+    if (p.N >= kLongSeq)
+      return use_dma(p) ? dkdv_pair_cfg<DP, SM, 4, 64, true, false, true>(p, st) : dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st);
     return bins_fit(p) ? dkdv_pair_cfg<DP, SM, 2, 64, false, true>(p, st) : dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
   }
 }
@@ -331,6 +348,8 @@ hipError_t dkdv_any_cfg(const Params& p, hipStream_t st) {
       case 23: return dkdv_pair_cfg<DP, SM, 2, 32>(p, st);
       case 25: return dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st);
       case 26: return dkdv_pair_cfg<DP, SM, 2, 64, true>(p, st);
+      case 27: return dkdv_pair_cfg<DP, SM, 4, 64, false, false, true>(p, st);
+      case 28: return dkdv_pair_cfg<DP, SM, 4, 64, true, false, true>(p, st);
       default: break;
     }
   }

@@ -405,6 +405,31 @@ def test_strided_views_like_the_model(cuda_device):
     compare_case(q, k, v, do, tag="strided")
 
 
+@pytest.mark.parametrize(
+    "N,dtype,softmax",
+    [(300, torch.bfloat16, True), (2113, torch.bfloat16, True), (2113, torch.float16, False)],
+)
+def test_strided_views_head_dim_128(cuda_device, N, dtype, softmax):
+    """D = 128 q/k/v as views of one packed projection and a permuted dout:
+    the tiles of the D = 128 kernels are staged by LDS-DMA through buffer
+    resources whose row pitch is the view's token stride (3 H D, or H D for
+    dout), and rows past N (N not a multiple of the 64-row tile) read zeros.
+    N = 300 takes the binned short-sequence kernels, N = 2113 the
+    long-sequence ones (paired dK/dV kernel).  Checked on the first and the
+    last (b, h) slice."""
+    B, H, D = 2, 3, 128
+    g = torch.Generator().manual_seed(N)
+    qkv = (torch.randn(B, N, 3 * H * D, generator=g) * (1.0 if softmax else 0.5)).to(dtype).to(cuda_device)
+    q, k, v = qkv.view(B, N, 3, H, D).permute(2, 0, 3, 1, 4)
+    do = torch.randn(B, N, H, D, generator=g).to(dtype).to(cuda_device).permute(0, 2, 1, 3)
+    assert not q.is_contiguous() and q.stride(2) == 3 * H * D and do.stride(2) == H * D
+    gamma = 1.0 / (2 * math.sqrt(D))
+    outs = run_ours(q, k, v, do, softmax, True, gamma, 0)
+    for sl in ((slice(0, 1), slice(0, 1)), (slice(B - 1, B), slice(H - 1, H))):
+        compare_case(q, k, v, do, softmax=softmax, gamma=gamma, sl=sl, outs=outs,
+                     tag=f"strided D128 N{N} b{sl[0].start}h{sl[1].start}")
+
+
 @pytest.mark.parametrize("softmax", [True, False])
 def test_one_launch_backward_equals_two_stages(cuda_device, softmax):
     """At B*H = 256 heads of N <= 576 the backward is one launch (both passes
