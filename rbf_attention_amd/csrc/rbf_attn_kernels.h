@@ -641,8 +641,7 @@ __device__ __forceinline__ uint32_t lds_addr(const T* p) {
 template <typename T, int ROWS, int W>
 struct DmaPair {
   static_assert(sizeof(T) == 2 && ROWS % 64 == 0, "DMA tiles: 16-bit, whole 64-row groups");
-  static constexpr int PER = (ROWS / 64) * 16, NI = 2 * PER, NIW = NI / W;
-  static_assert(NI % W == 0, "every wave issues the same number of DMA instructions");
+  static constexpr int PER = (ROWS / 64) * 16, NI = 2 * PER, NIW = (NI + W - 1) / W;
   i32x4_t ra, rb;
   uint32_t voff[NIW];  // lane byte offset of instruction j, tile row 0 at offset 0
   int loff[NIW];       // element offset of instruction j's 1 KB in its tile
@@ -657,7 +656,7 @@ struct DmaPair {
     rb = buffer_rsrc(B, (uint32_t)N * (uint32_t)rowb);
 #pragma unroll
     for (int j = 0; j < NIW; ++j) {
-      const int i = wave + j * W, k = i % PER, rg = k / 16, ch = k % 16;
+      const int i = min(wave + j * W, NI - 1), k = i % PER, rg = k / 16, ch = k % 16;
       const int row = i < PER ? rowa : rowb;
       voff[j] = (uint32_t)((64 * rg + lane) * row + 16 * ch);
       loff[j] = CLayout<ROWS>::off(64 * rg, 8 * ch);
@@ -668,8 +667,9 @@ struct DmaPair {
     const uint32_t la = lds_addr(tA), lb = lds_addr(tB);
 #pragma unroll
     for (int j = 0; j < NIW; ++j) {
-      // instruction wave + j * W reads slice A when below PER (known per j
-      // when W divides PER)
+      // instruction wave + j * W (if below NI) reads slice A when below PER
+      // (both known per j when W divides PER)
+      if (NI % W != 0 && wave + j * W >= NI) continue;
       const bool isa = PER % W == 0 ? j < PER / W : wave + j * W < PER;
       if (isa) dma16(voff[j] + (uint32_t)(tok0 * rowa), ra, la + 2u * (uint32_t)loff[j]);
       else dma16(voff[j] + (uint32_t)(tok0 * rowb), rb, lb + 2u * (uint32_t)loff[j]);
@@ -678,12 +678,15 @@ struct DmaPair {
 };
 
 // nrm[row] = -0.5 ||row||^2 (fp32, from the element-type values) of a landed
-// (ROWS x 128) chunk-major tile, -inf for tokens outside [0, N).  NT / ROWS
-// consecutive threads share a row.
+// (ROWS x 128) chunk-major tile, -inf for tokens outside [0, N).  TPR
+// consecutive threads share a row (the largest power of two <= NT / ROWS);
+// threads past ROWS * TPR have no row.
 template <typename T, int ROWS, int NT>
 __device__ __forceinline__ void tile_neg_halfnorms(const T* tile, float* nrm, int tok0, int N, int tid) {
-  constexpr int TPR = NT / ROWS, CPT = 16 / TPR;
-  static_assert(NT % ROWS == 0 && TPR <= 16 && 16 % TPR == 0, "threads per row must divide 16");
+  constexpr int Q = NT / ROWS;
+  constexpr int TPR = Q >= 16 ? 16 : Q >= 8 ? 8 : Q >= 4 ? 4 : Q >= 2 ? 2 : 1, CPT = 16 / TPR;
+  static_assert(Q >= 1, "at least one thread per row");
+  if (ROWS * TPR < NT && tid >= ROWS * TPR) return;
   const int row = tid / TPR, part = tid % TPR;
   float s = 0.f;
 #pragma unroll
