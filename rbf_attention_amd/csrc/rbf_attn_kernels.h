@@ -538,9 +538,11 @@ constexpr bool kChunkMajor = sizeof(T) == 2 && DP == 128;
 template <typename T, int ROWS, int DP, int NT>
 using TileFor = std::conditional_t<kChunkMajor<T, DP>, CTile<T, ROWS, DP, NT>, Tile<T, ROWS, DP, NT>>;
 
-template <typename T, int ROWS, int DP>
+// CMF: chunk-major whatever the default for (T, DP) (the LDS-DMA kernels,
+// whose DMA writes 64-row chunk columns).
+template <typename T, int ROWS, int DP, bool CMF = kChunkMajor<T, DP>>
 struct TileLayout {
-  static constexpr bool CM = kChunkMajor<T, DP>;
+  static constexpr bool CM = CMF;
   static constexpr int LDR = DP + Elem<T>::PAD;
   static constexpr int SIZE = CM ? CLayout<ROWS>::template size<DP>() : ROWS * LDR;
   __device__ static inline int off(int row, int col) {
@@ -631,17 +633,17 @@ __device__ __forceinline__ uint32_t lds_addr(const T* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) T*)p;
 }
 
-// The DMA of two (ROWS x 128) chunk-major tiles -- tokens tok0 .. tok0 +
-// ROWS - 1 of slices A and B, each (N, 128) with row stride sa / sb -- by W
-// waves: 2 * (ROWS / 64) * 16 instructions of 64 rows x one chunk, dealt
+// The DMA of two (ROWS x DP) chunk-major tiles -- tokens tok0 .. tok0 +
+// ROWS - 1 of slices A and B, each (N, DP) with row stride sa / sb -- by W
+// waves: 2 * (ROWS / 64) * (DP / 8) instructions of 64 rows x one chunk, dealt
 // round-robin to the waves.  A wave's lane offsets (relative to the tile's
 // first row) and LDS offsets are fixed, so a tile costs one add per
 // instruction.  Tokens outside [0, N) read zeros (buffer range check; the
 // host keeps N * stride * sizeof(T) below 2^31).
-template <typename T, int ROWS, int W>
+template <typename T, int ROWS, int DP, int W>
 struct DmaPair {
   static_assert(sizeof(T) == 2 && ROWS % 64 == 0, "DMA tiles: 16-bit, whole 64-row groups");
-  static constexpr int PER = (ROWS / 64) * 16, NI = 2 * PER, NIW = (NI + W - 1) / W;
+  static constexpr int CPR = DP / 8, PER = (ROWS / 64) * CPR, NI = 2 * PER, NIW = (NI + W - 1) / W;
   i32x4_t ra, rb;
   uint32_t voff[NIW];  // lane byte offset of instruction j, tile row 0 at offset 0
   int loff[NIW];       // element offset of instruction j's 1 KB in its tile
@@ -656,7 +658,7 @@ struct DmaPair {
     rb = buffer_rsrc(B, (uint32_t)N * (uint32_t)rowb);
 #pragma unroll
     for (int j = 0; j < NIW; ++j) {
-      const int i = min(wave + j * W, NI - 1), k = i % PER, rg = k / 16, ch = k % 16;
+      const int i = min(wave + j * W, NI - 1), k = i % PER, rg = k / CPR, ch = k % CPR;
       const int row = i < PER ? rowa : rowb;
       voff[j] = (uint32_t)((64 * rg + lane) * row + 16 * ch);
       loff[j] = CLayout<ROWS>::off(64 * rg, 8 * ch);
@@ -678,13 +680,14 @@ struct DmaPair {
 };
 
 // nrm[row] = -0.5 ||row||^2 (fp32, from the element-type values) of a landed
-// (ROWS x 128) chunk-major tile, -inf for tokens outside [0, N).  TPR
-// consecutive threads share a row (the largest power of two <= NT / ROWS);
-// threads past ROWS * TPR have no row.
-template <typename T, int ROWS, int NT>
+// (ROWS x DP) chunk-major tile, -inf for tokens outside [0, N).  TPR
+// consecutive threads share a row (the largest power of two <= NT / ROWS,
+// at most DP / 8); threads past ROWS * TPR have no row.
+template <typename T, int ROWS, int DP, int NT>
 __device__ __forceinline__ void tile_neg_halfnorms(const T* tile, float* nrm, int tok0, int N, int tid) {
-  constexpr int Q = NT / ROWS;
-  constexpr int TPR = Q >= 16 ? 16 : Q >= 8 ? 8 : Q >= 4 ? 4 : Q >= 2 ? 2 : 1, CPT = 16 / TPR;
+  constexpr int Q = NT / ROWS, CPR = DP / 8;
+  constexpr int TQ = Q >= 16 ? 16 : Q >= 8 ? 8 : Q >= 4 ? 4 : Q >= 2 ? 2 : 1;
+  constexpr int TPR = TQ < CPR ? TQ : CPR, CPT = CPR / TPR;
   static_assert(Q >= 1, "at least one thread per row");
   if (ROWS * TPR < NT && tid >= ROWS * TPR) return;
   const int row = tid / TPR, part = tid % TPR;
@@ -903,8 +906,8 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
   // transposing LDS reads; fp32 uses padded row-major K and a transposed copy
   // of V.
   constexpr bool TR = sizeof(T) == 2;
-  typedef TileLayout<T, BN, DP> TLy;
-  static_assert(!DMA || (TR && TLy::CM), "LDS-DMA staging is for chunk-major 16-bit tiles");
+  typedef TileLayout<T, BN, DP, DMA || kChunkMajor<T, DP>> TLy;
+  static_assert(!DMA || TR, "LDS-DMA staging is for 16-bit tiles");
   constexpr int TSZ = TLy::SIZE;
   // register staging: two buffers each (a single element when DMA)
   constexpr int NB2 = DMA ? 1 : 2;
@@ -1032,11 +1035,11 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
     };
     if constexpr (DMA) {
       auto tok0_of = [&](int kt) { return org + 32 * (kt * KB - kshift); };
-      DmaPair<T, BN, W> dma;
+      DmaPair<T, BN, DP, W> dma;
       dma.init(K, p.sk[2], V, p.sv[2], N, wave, lane);
       dma_pipeline(
           nkt, [&](int kt, int b) { dma.issue(tok0_of(kt), dK[b], dV[b]); },
-          [&](int kt, int b) { tile_neg_halfnorms<T, BN, NT>(dK[b], dN[b], tok0_of(kt), N, tid); },
+          [&](int kt, int b) { tile_neg_halfnorms<T, BN, DP, NT>(dK[b], dN[b], tok0_of(kt), N, tid); },
           [&](int kt, int b) { tile(kt, dK[b], dV[b], dN[b]); });
     } else {
       load_kv(0);
@@ -1124,8 +1127,8 @@ __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int gr
   // 16-bit types read K^T from the row-major K tile with transposing LDS
   // reads; fp32 stages a transposed copy.
   constexpr bool TR = sizeof(T) == 2;
-  typedef TileLayout<T, BN, DP> TLy;
-  static_assert(!DMA || (TR && TLy::CM), "LDS-DMA staging is for chunk-major 16-bit tiles");
+  typedef TileLayout<T, BN, DP, DMA || kChunkMajor<T, DP>> TLy;
+  static_assert(!DMA || TR, "LDS-DMA staging is for 16-bit tiles");
   constexpr int TSZ = TLy::SIZE;
   // register staging: two buffers each (a single element when DMA)
   constexpr int NB2 = DMA ? 1 : 2;
@@ -1291,11 +1294,11 @@ __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int gr
 
   auto tok0_of = [&](int kt) { return org + 32 * (kt * KB - kshift); };
   if constexpr (DMA) {
-    DmaPair<T, BN, W> dma;
+    DmaPair<T, BN, DP, W> dma;
     dma.init(K, p.sk[2], V, p.sv[2], N, wave, lane);
     dma_pipeline(
         nkt, [&](int kt, int b) { dma.issue(tok0_of(kt), dK[b], dV[b]); },
-        [&](int kt, int b) { tile_neg_halfnorms<T, BN, NT>(dK[b], dN[b], tok0_of(kt), N, tid); },
+        [&](int kt, int b) { tile_neg_halfnorms<T, BN, DP, NT>(dK[b], dN[b], tok0_of(kt), N, tid); },
         [&](int kt, int b) { tile(kt, dK[b], nullptr, dV[b], dN[b]); });
   } else {
     TileFor<T, BN, DP, NT> tk, tv;
@@ -1369,8 +1372,10 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dq_kernel(const Params p) {
 //   dP = dO V^T (init -Delta), dS = P dP,
 //   dV^T += dO^T P, dK^T += Q^T dS, colsum += sum_i dS.
 // ---------------------------------------------------------------------------
+// DMA: Q and dO tiles, and the raw L and Delta rows, staged by LDS-DMA
+// (dma_pipeline; 16-bit, D = DP only).
 template <typename T, int DP, int W, int KPW, int BM, bool SOFTMAX, bool EARLY = true, bool PIPE = false,
-          bool PRIO = false>
+          bool PRIO = false, bool DMA = false>
 __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int grp) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -1379,15 +1384,24 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
   // 16-bit types read Q^T and dO^T from the row-major tiles with transposing
   // LDS reads; fp32 stages transposed copies.
   constexpr bool TR = sizeof(T) == 2;
-  typedef TileLayout<T, BM, DP> TLy;
+  typedef TileLayout<T, BM, DP, DMA || kChunkMajor<T, DP>> TLy;
+  static_assert(!DMA || (TR && BM % 64 == 0), "LDS-DMA staging: 16-bit tiles of whole 64-row groups");
   constexpr int TSZ = TLy::SIZE;
-  __shared__ __attribute__((aligned(16))) T sQ[2][TSZ];
+  // register staging: two buffers each; LDS-DMA staging: three (the other
+  // form's arrays shrink to a single element)
+  constexpr int NB2 = DMA ? 1 : 2, NB3 = DMA ? 3 : 1;
+  __shared__ __attribute__((aligned(16))) T sQ[NB2][DMA ? 8 : TSZ];
   __shared__ __attribute__((aligned(16))) T sQt[TR ? 1 : 2][TR ? 8 : DP * LDT];
-  __shared__ __attribute__((aligned(16))) T sD[2][TSZ];
+  __shared__ __attribute__((aligned(16))) T sD[NB2][DMA ? 8 : TSZ];
   auto roff = [](int row, int col) { return TLy::off(row, col); };
   __shared__ __attribute__((aligned(16))) T sDt[TR ? 1 : 2][TR ? 8 : DP * LDT];
-  __shared__ __attribute__((aligned(16))) float sOff[2][BM];
-  __shared__ __attribute__((aligned(16))) float sDel[2][BM];
+  __shared__ __attribute__((aligned(16))) float sOff[NB2][DMA ? 1 : BM];
+  __shared__ __attribute__((aligned(16))) float sDel[NB2][DMA ? 1 : BM];
+  __shared__ __attribute__((aligned(16))) T dQt[NB3][DMA ? TSZ : 8];
+  __shared__ __attribute__((aligned(16))) T dDt[NB3][DMA ? TSZ : 8];
+  __shared__ __attribute__((aligned(16))) float dOff[NB3][DMA ? BM : 1];
+  __shared__ __attribute__((aligned(16))) float dDel[NB3][DMA ? BM : 1];
+  __shared__ __attribute__((aligned(16))) float dRaw[NB3][2][DMA ? BM : 1];  // L, Delta as loaded
 
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1465,25 +1479,12 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
       if constexpr (SOFTMAX) delr = ok ? -delg[tok] : 0.f;
     }
   };
-  load_tile(qt_lo);
-  for (int qt = qt_lo; qt < nqt_all; ++qt) {
-    const int buf = qt & 1;
-    if constexpr (TR) {
-      TLy::store(tq, sQ[buf], tid);
-      TLy::store(td, sD[buf], tid);
-    } else {
-      tq.template store_rows<LDR>(sQ[buf], tid);
-      td.template store_rows<LDR>(sD[buf], tid);
-      tq.template store_trans<LDT>(sQt[buf], tid);
-      td.template store_trans<LDT>(sDt[buf], tid);
-    }
-    if (tid < BM) {
-      sOff[buf][tid] = offr;
-      sDel[buf][tid] = delr;
-    }
-    __syncthreads();
-    if (qt + 1 < nqt_all) load_tile(qt + 1);
-    if (!wave_on) continue;
+  // Query tile qt against this wave's key blocks, from tiles sQb (Q), sDb
+  // (dO), sQtb / sDtb (their transposes, fp32 only) and per-query terms offb
+  // (-L/c), delb (-Delta).
+  auto tile = [&](int qt, const T* sQb, const T* sDb, const T* sQtb, const T* sDtb, const float* offb,
+                  const float* delb) {
+    if (!wave_on) return;
     const int qblk0 = qt * QB - qshift;
     if constexpr (PIPE && KPW == 1) {
       // Fast path for tiles whose every (query block, key block) pair is fully
@@ -1501,13 +1502,13 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
         f32x16_t sacc[QB], dpacc[QB];
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-          sacc[qb] = ld_rows16(sOff[buf] + 32 * qb, h);
-          if constexpr (SOFTMAX) dpacc[qb] = ld_rows16(sDel[buf] + 32 * qb, h);
+          sacc[qb] = ld_rows16(offb + 32 * qb, h);
+          if constexpr (SOFTMAX) dpacc[qb] = ld_rows16(delb + 32 * qb, h);
           else dpacc[qb] = zero16();
 #pragma unroll
           for (int t = 0; t < KS; ++t) {
-            const frag qA = ld8<T>(sQ[buf] + roff(32 * qb + n, 16 * t + 8 * h));
-            const frag dA = ld8<T>(sD[buf] + roff(32 * qb + n, 16 * t + 8 * h));
+            const frag qA = ld8<T>(sQb + roff(32 * qb + n, 16 * t + 8 * h));
+            const frag dA = ld8<T>(sDb + roff(32 * qb + n, 16 * t + 8 * h));
             sacc[qb] = E::mma(qA, kf[0][t], sacc[qb]);
             dpacc[qb] = E::mma(dA, vf[0][t], dpacc[qb]);
           }
@@ -1530,18 +1531,18 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
             for (int t = 0; t < 2; ++t) {
               frag dtA, qtA;
               if constexpr (TR) {
-                dtA = TLy::tr(sD[buf], 32 * qb + 16 * t, 32 * d, lane);
-                qtA = TLy::tr(sQ[buf], 32 * qb + 16 * t, 32 * d, lane);
+                dtA = TLy::tr(sDb, 32 * qb + 16 * t, 32 * d, lane);
+                qtA = TLy::tr(sQb, 32 * qb + 16 * t, 32 * d, lane);
               } else {
                 const int o = (32 * d + n) * LDT + tchunk<BM>(32 * d + n, 32 * qb + 16 * t + 8 * h);
-                dtA = ld8<T>(sDt[buf] + o);
-                qtA = ld8<T>(sQt[buf] + o);
+                dtA = ld8<T>(sDtb + o);
+                qtA = ld8<T>(sQtb + o);
               }
               dvacc[0][d] = E::mma(dtA, pf[t], dvacc[0][d]);
               dkacc[0][d] = E::mma(qtA, sf[t], dkacc[0][d]);
             }
         }
-        continue;
+        return;
       }
     }
 #pragma unroll
@@ -1558,12 +1559,12 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
       frag qA[KS], dA[KS];
 #pragma unroll
       for (int t = 0; t < KS; ++t) {
-        qA[t] = ld8<T>(sQ[buf] + roff(32 * qb + n, 16 * t + 8 * h));
-        dA[t] = ld8<T>(sD[buf] + roff(32 * qb + n, 16 * t + 8 * h));
+        qA[t] = ld8<T>(sQb + roff(32 * qb + n, 16 * t + 8 * h));
+        dA[t] = ld8<T>(sDb + roff(32 * qb + n, 16 * t + 8 * h));
       }
-      const f32x16_t oinit = ld_rows16(sOff[buf] + 32 * qb, h);
+      const f32x16_t oinit = ld_rows16(offb + 32 * qb, h);
       f32x16_t dinit;
-      if constexpr (SOFTMAX) dinit = ld_rows16(sDel[buf] + 32 * qb, h);
+      if constexpr (SOFTMAX) dinit = ld_rows16(delb + 32 * qb, h);
       else dinit = zero16();
       f32x16_t sacc[KPW], dpacc[KPW];
       if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
@@ -1588,12 +1589,12 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
             if constexpr (TR) {
-              dtA[d][t] = TLy::tr(sD[buf], 32 * qb + 16 * t, 32 * d, lane);
-              qtA[d][t] = TLy::tr(sQ[buf], 32 * qb + 16 * t, 32 * d, lane);
+              dtA[d][t] = TLy::tr(sDb, 32 * qb + 16 * t, 32 * d, lane);
+              qtA[d][t] = TLy::tr(sQb, 32 * qb + 16 * t, 32 * d, lane);
             } else {
               const int o = (32 * d + n) * LDT + tchunk<BM>(32 * d + n, 32 * qb + 16 * t + 8 * h);
-              dtA[d][t] = ld8<T>(sDt[buf] + o);
-              qtA[d][t] = ld8<T>(sQt[buf] + o);
+              dtA[d][t] = ld8<T>(sDtb + o);
+              qtA[d][t] = ld8<T>(sQtb + o);
             }
           }
       };
@@ -1629,6 +1630,59 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
             }
       if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     }
+  };
+  if constexpr (DMA) {
+    // The tile's raw L and Delta are DMA'd with it (the last wave issues
+    // them) and turned into -L/c and -Delta by the first waves once landed.
+    DmaPair<T, BM, DP, W> dma;
+    dma.init(Q, p.sq[2], dO, p.sdo[2], N, wave, lane);
+    const i32x4_t roffr = buffer_rsrc(offg, 4u * (uint32_t)N);
+    const i32x4_t rdelr = buffer_rsrc(SOFTMAX ? delg : offg, 4u * (uint32_t)N);
+    auto tok0_of = [&](int qt) { return org + 32 * (qt * QB - qshift); };
+    dma_pipeline(
+        nqt_all - qt_lo,
+        [&](int t, int b) {
+          const int tok0 = tok0_of(qt_lo + t);
+          dma.issue(tok0, dQt[b], dDt[b]);
+          if (wave == W - 1) {
+#pragma unroll
+            for (int r = 0; r < BM / 64; ++r) {
+              const uint32_t vo = 4u * (uint32_t)(tok0 + 64 * r + lane);  // negative tokens: out of range
+              dma4(vo, roffr, lds_addr(&dRaw[b][0][64 * r]));
+              if constexpr (SOFTMAX) dma4(vo, rdelr, lds_addr(&dRaw[b][1][64 * r]));
+            }
+          }
+        },
+        [&](int t, int b) {
+          if (tid < BM) {
+            const int tok = tok0_of(qt_lo + t) + tid;
+            const bool ok = tok >= 0 && tok < N;
+            dOff[b][tid] = ok ? -dRaw[b][0][tid] * inv_c : -__builtin_inff();  // padding queries: P = 0
+            dDel[b][tid] = (SOFTMAX && ok) ? -dRaw[b][1][tid] : 0.f;
+          }
+        },
+        [&](int t, int b) { tile(qt_lo + t, dQt[b], dDt[b], nullptr, nullptr, dOff[b], dDel[b]); });
+  } else {
+    load_tile(qt_lo);
+    for (int qt = qt_lo; qt < nqt_all; ++qt) {
+      const int buf = qt & 1;
+      if constexpr (TR) {
+        TLy::store(tq, sQ[buf], tid);
+        TLy::store(td, sD[buf], tid);
+      } else {
+        tq.template store_rows<LDR>(sQ[buf], tid);
+        td.template store_rows<LDR>(sD[buf], tid);
+        tq.template store_trans<LDT>(sQt[buf], tid);
+        td.template store_trans<LDT>(sDt[buf], tid);
+      }
+      if (tid < BM) {
+        sOff[buf][tid] = offr;
+        sDel[buf][tid] = delr;
+      }
+      __syncthreads();
+      if (qt + 1 < nqt_all) load_tile(qt + 1);
+      tile(qt, sQ[buf], sD[buf], sQt[TR ? 0 : buf], sDt[TR ? 0 : buf], sOff[buf], sDel[buf]);
+    }
   }
 
   if (!wave_on) return;
@@ -1661,10 +1715,10 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
 }
 
 template <typename T, int DP, int W, int KPW, int BM, bool SOFTMAX, bool EARLY = true, bool PIPE = false,
-          bool PRIO = false, bool BIN = false>
+          bool PRIO = false, bool BIN = false, bool DMA = false>
 __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
   for_each_group<BIN>(p, (p.nblk + W * KPW - 1) / (W * KPW), false,
-                 [&](int bh, int grp) { rbf_bwd_dkdv_group<T, DP, W, KPW, BM, SOFTMAX, EARLY, PIPE, PRIO>(p, bh, grp); });
+                 [&](int bh, int grp) { rbf_bwd_dkdv_group<T, DP, W, KPW, BM, SOFTMAX, EARLY, PIPE, PRIO, DMA>(p, bh, grp); });
 }
 
 // ---------------------------------------------------------------------------
@@ -1880,7 +1934,7 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
       static_assert(!DMA || BM == 64, "one 64-lane DMA per per-query term");
       // The tile's raw L and Delta are DMA'd with it (the last wave issues
       // them) and turned into -L/c and -Delta by the first wave once landed.
-      DmaPair<T, BM, W> dma;
+      DmaPair<T, BM, DP, W> dma;
       dma.init(Q, p.sq[2], dO, p.sdo[2], N, wave, lane);
       const i32x4_t roff = buffer_rsrc(offg, 4u * (uint32_t)N);
       const i32x4_t rdel = buffer_rsrc(SOFTMAX ? delg : offg, 4u * (uint32_t)N);

@@ -154,14 +154,15 @@ bool use_hr(const Params& p, int nb_max, int which) {
 }
 constexpr int kHrBlocks64 = kHrMaxBlocks;  // D <= 64: N <= 576
 
-// LDS-DMA tile staging (16-bit, D = 128: the streaming kernels' tiles go from
-// global memory straight into LDS, three tiles in flight).  The DMA reads
-// through buffer resources whose byte range (N rows of each slice) must stay
-// below 2^31.  RBF_ATTN_DMA=0 keeps the register-staged kernels.
+// LDS-DMA tile staging (16-bit, D = 64 or 128 filling the padded width DP:
+// the streaming kernels' tiles go from global memory straight into LDS, three
+// tiles in flight).  The DMA reads whole DP-wide rows through buffer
+// resources whose byte range (N rows of each slice) must stay below 2^31.
+// RBF_ATTN_DMA=0 keeps the register-staged kernels.
 bool dma_fits(int64_t N, int64_t stride) { return N * stride * (int64_t)sizeof(Elt) < (int64_t(1) << 31); }
-bool use_dma(const Params& p) {
+bool use_dma(const Params& p, int dp) {
   static const int forced = env_choice("RBF_ATTN_DMA");
-  return !kIsF32 && forced != 0 && p.D == 128 && dma_fits(p.N, p.sk[2]) && dma_fits(p.N, p.sv[2]) &&
+  return !kIsF32 && forced != 0 && p.D == dp && dma_fits(p.N, p.sk[2]) && dma_fits(p.N, p.sv[2]) &&
          dma_fits(p.N, p.sq[2]) && dma_fits(p.N, p.sdo[2]);
 }
 
@@ -180,9 +181,9 @@ hipError_t dq_cfg(const Params& p, hipStream_t st) {
 }
 
 template <int DP, bool SM, int W, int KPW, int BM, bool EARLY = true, bool PIPE = false, bool PRIO = false,
-          bool BIN = false>
+          bool BIN = false, bool DMA = false>
 hipError_t dkdv_cfg(const Params& p, hipStream_t st) {
-  auto k = rbf_bwd_dkdv_kernel<Elt, DP, W, KPW, BM, SM, EARLY, PIPE, PRIO, BIN>;
+  auto k = rbf_bwd_dkdv_kernel<Elt, DP, W, KPW, BM, SM, EARLY, PIPE, PRIO, BIN, DMA>;
   static const int wgs = wgs_per_cu(k, 64 * W);
   return launch(k, p, W * KPW, 64 * W, wgs, BIN, st);
 }
@@ -217,10 +218,15 @@ hipError_t fwd_default(const Params& p, hipStream_t st) {
   }
   if constexpr (kIsF32) return fwd_cfg<DP, SM, 4, 32>(p, st);
   else if constexpr (DP <= 64) {
+    if (DP == 64 && use_dma(p, DP)) {
+      if (p.N >= kLongSeq)
+        return bins_fit(p) ? fwd_cfg<DP, SM, 8, 128, true, true>(p, st) : fwd_cfg<DP, SM, 8, 128, false, true>(p, st);
+      return bins_fit(p) ? fwd_cfg<DP, SM, 4, 64, true, true>(p, st) : fwd_cfg<DP, SM, 4, 64, false, true>(p, st);
+    }
     if (p.N >= kLongSeq) return bins_fit(p) ? fwd_cfg<DP, SM, 8, 128, true>(p, st) : fwd_cfg<DP, SM, 8, 128>(p, st);
     return bins_fit(p) ? fwd_cfg<DP, SM, 4, 64, true>(p, st) : fwd_cfg<DP, SM, 4, 64>(p, st);
   } else {
-    if (use_dma(p)) return bins_fit(p) ? fwd_cfg<DP, SM, 8, 64, true, true>(p, st) : fwd_cfg<DP, SM, 8, 64, false, true>(p, st);
+    if (use_dma(p, DP)) return bins_fit(p) ? fwd_cfg<DP, SM, 8, 64, true, true>(p, st) : fwd_cfg<DP, SM, 8, 64, false, true>(p, st);
     return bins_fit(p) ? fwd_cfg<DP, SM, 8, 64, true>(p, st) : fwd_cfg<DP, SM, 8, 64>(p, st);
   }
 }
@@ -237,10 +243,15 @@ hipError_t dq_default(const Params& p, hipStream_t st) {
     if (use_hr(p, kHrBlocks64, 2)) return hr_dq(p, SM, st);
   }
   if constexpr (kIsF32) return dq_cfg<DP, SM, 4, 1, 32>(p, st);
-  else if constexpr (DP <= 64)
+  else if constexpr (DP <= 64) {
+    // (LDS-DMA on 64-key tiles: three 128-key tiles leave room for one
+    // four-wave work-group per CU)
+    if (DP == 64 && use_dma(p, DP))
+      return bins_fit(p) ? dq_cfg<DP, SM, 4, 1, 64, true, true, true>(p, st) : dq_cfg<DP, SM, 4, 1, 64, true, false, true>(p, st);
     return bins_fit(p) ? dq_cfg<DP, SM, 4, 1, 128, true, true>(p, st) : dq_cfg<DP, SM, 4, 1, 128>(p, st);
+  }
   else {
-    if (use_dma(p))
+    if (use_dma(p, DP))
       return bins_fit(p) ? dq_cfg<DP, SM, 8, 1, 64, true, true, true>(p, st) : dq_cfg<DP, SM, 8, 1, 64, true, false, true>(p, st);
     return bins_fit(p) ? dq_cfg<DP, SM, 8, 1, 32, true, true>(p, st) : dq_cfg<DP, SM, 8, 1, 32>(p, st);
   }
@@ -259,6 +270,11 @@ hipError_t dkdv_default(const Params& p, hipStream_t st) {
   }
   if constexpr (kIsF32) return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
   else if constexpr (DP <= 64) {
+    // LDS-DMA from N = 4096 on: at N = 512-2048 the D = 64 dK/dV measured as
+    // fast or slower with it (C4 188 -> 191 us), at N = 8192 faster (605 -> 589)
+    if (DP == 64 && p.N >= 2 * kLongSeq && use_dma(p, DP))
+      return bins_fit(p) ? dkdv_cfg<DP, SM, 8, 1, 128, true, false, false, true, true>(p, st)
+                         : dkdv_cfg<DP, SM, 8, 1, 128, true, false, false, false, true>(p, st);
     if (p.N >= kLongSeq)
       return bins_fit(p) ? dkdv_cfg<DP, SM, 8, 1, 128, true, false, false, true>(p, st) : dkdv_cfg<DP, SM, 8, 1, 128>(p, st);
     return bins_fit(p) ? dkdv_cfg<DP, SM, 4, 1, 128, false, false, false, true>(p, st)
@@ -267,7 +283,7 @@ hipError_t dkdv_default(const Params& p, hipStream_t st) {
     // the long-sequence paired kernel measured slower with the bin loop
     // (LDS-DMA for long sequences only: the two-pair binned form spills with it)
     if (p.N >= kLongSeq)
-      return use_dma(p) ? dkdv_pair_cfg<DP, SM, 4, 64, true, false, true>(p, st) : dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st);
+      return use_dma(p, DP) ? dkdv_pair_cfg<DP, SM, 4, 64, true, false, true>(p, st) : dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st);
     return bins_fit(p) ? dkdv_pair_cfg<DP, SM, 2, 64, false, true>(p, st) : dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
   }
 }

@@ -406,18 +406,21 @@ def test_strided_views_like_the_model(cuda_device):
 
 
 @pytest.mark.parametrize(
-    "N,dtype,softmax",
-    [(300, torch.bfloat16, True), (2113, torch.bfloat16, True), (2113, torch.float16, False)],
+    "D,N,dtype,softmax",
+    [(128, 300, torch.bfloat16, True), (128, 2113, torch.bfloat16, True), (128, 2113, torch.float16, False),
+     (64, 700, torch.bfloat16, True), (64, 4200, torch.bfloat16, True), (64, 4200, torch.float16, False)],
 )
-def test_strided_views_head_dim_128(cuda_device, N, dtype, softmax):
-    """D = 128 q/k/v as views of one packed projection and a permuted dout:
-    the tiles of the D = 128 kernels are staged by LDS-DMA through buffer
-    resources whose row pitch is the view's token stride (3 H D, or H D for
-    dout), and rows past N (N not a multiple of the 64-row tile) read zeros.
-    N = 300 takes the binned short-sequence kernels, N = 2113 the
-    long-sequence ones (paired dK/dV kernel).  Checked on the first and the
-    last (b, h) slice."""
-    B, H, D = 2, 3, 128
+def test_strided_views_dma_tiles(cuda_device, D, N, dtype, softmax):
+    """q/k/v as views of one packed projection and a permuted dout, for the
+    streaming kernels whose tiles are staged by LDS-DMA (16-bit, D = 64 or
+    128) through buffer resources whose row pitch is the view's token stride
+    (3 H D, or H D for dout); rows past N (N not a multiple of the 64-row
+    tile) read zeros.  D = 128: N = 300 takes the binned short-sequence
+    kernels, N = 2113 the long-sequence ones (paired dK/dV kernel); D = 64
+    (B * H below the CU count, so no head-resident kernels): N = 700 DMA
+    forward and dQ, N = 4200 also the DMA dK/dV.  Checked on the first and
+    the last (b, h) slice."""
+    B, H = 2, 3
     g = torch.Generator().manual_seed(N)
     qkv = (torch.randn(B, N, 3 * H * D, generator=g) * (1.0 if softmax else 0.5)).to(dtype).to(cuda_device)
     q, k, v = qkv.view(B, N, 3, H, D).permute(2, 0, 3, 1, 4)
@@ -427,7 +430,7 @@ def test_strided_views_head_dim_128(cuda_device, N, dtype, softmax):
     outs = run_ours(q, k, v, do, softmax, True, gamma, 0)
     for sl in ((slice(0, 1), slice(0, 1)), (slice(B - 1, B), slice(H - 1, H))):
         compare_case(q, k, v, do, softmax=softmax, gamma=gamma, sl=sl, outs=outs,
-                     tag=f"strided D128 N{N} b{sl[0].start}h{sl[1].start}")
+                     tag=f"strided D{D} N{N} b{sl[0].start}h{sl[1].start}")
 
 
 @pytest.mark.parametrize("softmax", [True, False])
