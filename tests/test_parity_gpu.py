@@ -288,6 +288,22 @@ def test_masks(cuda_device, causal, num_prefix, softmax):
                  tag=f"mask c{causal} p{num_prefix}")
 
 
+@pytest.mark.parametrize(
+    "D,N,dtype,softmax,causal,num_prefix",
+    [(128, 2200, torch.bfloat16, True, False, 0), (128, 2200, torch.bfloat16, True, True, 40),
+     (128, 2200, torch.float16, False, True, 300), (64, 4300, torch.bfloat16, True, False, 0),
+     (64, 4300, torch.bfloat16, False, True, 300), (64, 4300, torch.float16, True, True, 4)],
+)
+def test_masks_long(cuda_device, D, N, dtype, softmax, causal, num_prefix):
+    """Non-causal and register-token masks on the long-sequence streaming
+    kernels with LDS-DMA tiles (D = 128: paired dK/dV kernel; D = 64: DMA
+    dK/dV from N = 4096), whose query-tile ranges start at the first tile when
+    keys are visible to every query."""
+    q, k, v, do = rand_inputs(1, 1, N, D, dtype, cuda_device, std=1.0 if softmax else 0.5, seed=N + D + num_prefix)
+    compare_case(q, k, v, do, softmax=softmax, causal=causal, num_prefix=num_prefix, gamma=1.0 / (2 * math.sqrt(D)),
+                 tag=f"mask long D{D} N{N} {dtype} sm{softmax} c{causal} p{num_prefix}")
+
+
 @pytest.mark.parametrize("D", [64, 128])
 def test_heavy_tailed_keys(cuda_device, D):
     q, k, v, do = rand_inputs(2, 4, 300, D, torch.bfloat16, cuda_device, seed=11, key_scale=0.5)
