@@ -249,6 +249,9 @@ def setup_workload(w, dev):
     return bufs, make_args(_lib, w, bufs, variant)
 
 
+GRAPH_STEPS = 10  # steps per captured HIP graph (graph_step_us)
+
+
 def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold_reps: int, graph: bool):
     """Step, per-kernel and cold-cache timings of one workload through the C
     ABI; returns (result dict, step ms)."""
@@ -287,8 +290,10 @@ def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold
 
     ms_graph = None
     if graph:
-        # The same step captured once in a HIP graph and replayed; reported
-        # beside the eager step, not as it.
+        # GRAPH_STEPS steps captured in one HIP graph and replayed; reported
+        # per step, beside the eager step, not as it.  Several steps per
+        # graph separate the graph launch's own cost from the time added
+        # between kernel nodes.
         def cur_step():
             s = torch.cuda.current_stream(dev).cuda_stream
             _lib.call("rbf_attn_fwd", a, s)
@@ -297,10 +302,11 @@ def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold
         try:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                cur_step()
+                for _ in range(GRAPH_STEPS):
+                    cur_step()
             g.replay()
-            ms_graph = timer.loop(g.replay, steps)
-            log(f"  graph step: {ms_graph * 1e3:.2f} us")
+            ms_graph = timer.loop(g.replay, max(1, steps // GRAPH_STEPS)) / GRAPH_STEPS
+            log(f"  graph step: {ms_graph * 1e3:.2f} us ({GRAPH_STEPS} steps per graph)")
         except RuntimeError as e:  # reported as null; the eager measurement stands
             log(f"  graph step: capture failed ({e})")
 
