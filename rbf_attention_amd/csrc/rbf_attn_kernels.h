@@ -715,8 +715,11 @@ __device__ __forceinline__ void dma_pipeline(int nt, Issue&& issue, Land&& land,
     wait_vmem();
     lds_barrier();
     if (t + 2 < nt) issue(t + 2, b2);
-    if (t + 1 < nt) land(t + 1, b1);
+    // tile t + 1's terms after tile t's compute (they are used only after
+    // the next barrier): waves that finish their blocks early do this work
+    // while the others still compute.
     compute(t, b0);
+    if (t + 1 < nt) land(t + 1, b1);
     const int b = b0;
     b0 = b1;
     b1 = b2;
