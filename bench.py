@@ -23,6 +23,10 @@ Timing protocol
     write that evicts L2 and MALL (outside the events).
   * `kernel_us`: each kernel of the step in an event-timed loop of its own;
     the roofline entry is computed from the dominant one.
+  * `op_step_us`: the same step through the torch ops instead of the C ABI
+    (run_triton_rbf / run_triton_non_softmax_rbf forward, then backward through
+    their autograd): Python dispatch and the outputs, L and gradients from
+    torch's caching allocator on top of the same kernels.
 """
 from __future__ import annotations
 
@@ -310,6 +314,25 @@ def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold
         except RuntimeError as e:  # reported as null; the eager measurement stands
             log(f"  graph step: capture failed ({e})")
 
+    # The same step through the torch ops (the rbf_attn_v5 / rbf_attn_amd ops
+    # and their autograd): Python dispatch, output, L and gradient tensors
+    # from torch's caching allocator, then the same kernels.
+    import rbf_attention_amd as ra
+
+    op_fn = ra.run_triton_rbf if w.softmax else ra.run_triton_non_softmax_rbf
+    oq, ok_, ov = (bufs[n].detach().clone().requires_grad_(True) for n in ("q", "k", "v"))
+
+    def op_step():
+        oq.grad = ok_.grad = ov.grad = None
+        op_fn(oq, ok_, ov, w.causal, sm_scale=w.sm_scale).backward(bufs["dout"])
+
+    with torch.cuda.stream(timer.stream):
+        for _ in range(max(3, warmup // 10)):
+            op_step()
+        ms_op = timer.loop(op_step, steps)
+    del oq, ok_, ov
+    log(f"  op-level step (torch ops + autograd): {ms_op * 1e3:.2f} us")
+
     # Per-kernel averages, each kernel in a loop of its own (events between
     # single launches add their own cost to every launch).  With a one-launch
     # backward its two stages are timed too, for reference.
@@ -338,6 +361,7 @@ def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold
             "flush": f"{FLUSH_MIB} MiB write before each rep, outside the events",
         },
         "graph_step_us": round(ms_graph * 1e3, 3) if ms_graph is not None else None,
+        "op_step_us": round(ms_op * 1e3, 3),
         "kernel_us": {kk: round(t * 1e3, 3) for kk, t in kern_ms.items()},
         "step_kernels": list(step_kernels),
         "roofline": roofline(w, dom, per_pair[dom] * w.D * P, kern_ms[dom] * 1e-3, peak),
@@ -605,6 +629,7 @@ def main() -> int:
         "clock_ramp_s": args.ramp_seconds,
         "cold": head["cold"],
         "graph_step_us": head["graph_step_us"],
+        "op_step_us": head["op_step_us"],
         "kernel_us": head["kernel_us"],
         "step_kernels": head["step_kernels"],
         "roofline": head["roofline"],

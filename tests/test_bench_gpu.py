@@ -43,6 +43,8 @@ def test_bench_json_line(cuda_device):
     assert r["value"] > 0 and r["ms_per_step"] > 0
     check_roofline(r["roofline"], r["step_kernels"])
     assert r["cold"]["step_us_median"] > 0 and r["cold"]["reps"] == 3
+    # the op-level step runs the same kernels plus Python dispatch and allocation
+    assert r["op_step_us"] >= 0.9 * r["ms_per_step"] * 1e3
     # the forward keeps out (B,H,N,D bf16) and L (B,H,N fp32) for backward
     expect = (32 * 8 * 516 * 64 * 2 + 32 * 8 * 516 * 4) / 2 ** 20
     assert r["peak_fwd_activation_mb"] == pytest.approx(expect, rel=0.05)
@@ -66,5 +68,6 @@ def test_bench_extra_configs(cuda_device):
         c = r[key]
         assert c["config"]["workload"] == wname
         assert c["step_us"] > 0 and c["tflops"] > 0 and c["cold"]["step_us_median"] > 0
+        assert c["op_step_us"] >= 0.9 * c["step_us"]
         assert c["roofline"]["bound"] == "mfma"
         check_roofline(c["roofline"], c["step_kernels"])
