@@ -23,6 +23,9 @@ Timing protocol
     write that evicts L2 and MALL (outside the events).
   * `kernel_us`: each kernel of the step in an event-timed loop of its own;
     the roofline entry is computed from the dominant one.
+  * `native_harness`: the same step timed by rbf_attn_bench, a C++ program
+    that calls the C ABI directly (no Python), in a child process, with the
+    same protocol (ramp, warm-up, K steps between events, cold reps).
   * `op_step_us`: the same step through the torch ops instead of the C ABI
     (run_triton_rbf / run_triton_non_softmax_rbf forward, then backward through
     their autograd): Python dispatch and the outputs, L and gradients from
@@ -560,6 +563,22 @@ def decode_bench(dev, iters: int):
     }
 
 
+def native_harness(workload: str, steps: int, warmup: int, cold_reps: int, ramp_s: float) -> dict:
+    """The same step timed by rbf_attn_bench, the C++ harness that calls the
+    C ABI directly (built next to librbfattn.so), as a child process."""
+    import subprocess
+
+    exe = os.path.join(REPO, "rbf_attention_amd", "rbf_attn_bench")
+    if not os.path.exists(exe):
+        return {"error": f"{exe} not built (python -m rbf_attention_amd.build)"}
+    cmd = [exe, "--workload", workload, "--steps", str(steps), "--warmup", str(warmup), "--cold-reps",
+           str(cold_reps), "--ramp-seconds", str(ramp_s)]
+    p = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
+    if p.returncode != 0:
+        return {"error": f"rc={p.returncode}: {p.stderr.strip()[-500:]}"}
+    return json.loads(p.stdout.strip().splitlines()[-1])
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -578,6 +597,7 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true", help="skip the KV-cache decode measurement")
     ap.add_argument("--no-extra-configs", action="store_true", help="skip the C3/C4 objects")
     ap.add_argument("--no-ref-sweep", action="store_true", help="skip the reference's own fp16 length sweep")
+    ap.add_argument("--no-native", action="store_true", help="skip the C++ harness (rbf_attn_bench) timings")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="run one device copy of this many MiB before timing (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -635,11 +655,17 @@ def main() -> int:
         "roofline": head["roofline"],
         "peak_fwd_activation_mb": peak_fwd_mb(dev, w),
     }
+    if not args.no_native:
+        log("native harness (C++, C ABI) ...")
+        result["native_harness"] = native_harness(w.name, args.steps, args.warmup, args.cold_reps, args.ramp_seconds)
+        log(f"  {result['native_harness']}")
     if not args.no_extra_configs:
         for name in ("c3_long_bf16", "c4_nonsoftmax_bf16"):
             if name == w.name:
                 continue
             r, _ = measure_workload(wl.CONFIGS[name], dev, timer, 20, 5, 0.2, 5, graph=False)
+            if not args.no_native and name == "c3_long_bf16":
+                r["native_harness"] = native_harness(name, 20, 5, 5, 0.2)
             result[name.split("_")[0]] = r
             torch.cuda.empty_cache()
     if not args.no_ref_sweep:

@@ -21,6 +21,10 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_NAME = "librbfattn.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+# Native timing harness of the C ABI (csrc/rbf_attn_bench.cpp), linked
+# against the library next to it.
+BENCH_NAME = "rbf_attn_bench"
+BENCH_PATH = os.path.join(PKG_DIR, BENCH_NAME)
 ARCH = os.environ.get("RBF_ATTN_ARCH", "gfx950")
 
 # Packed-FP32 VALU ops are disabled for all device code.  MFMA accumulators
@@ -90,8 +94,15 @@ def build(verbose: bool = True) -> str:
         _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp_lib, *[o for _, o in jobs]])
         shutil.copyfile(tmp_lib, LIB_PATH + ".tmp")
         os.replace(LIB_PATH + ".tmp", LIB_PATH)
+        tmp_bench = os.path.join(tmp, BENCH_NAME)
+        _run([hipcc, f"--offload-arch={ARCH}", "-O2", "-std=c++17", f"-I{INCLUDE}",
+              os.path.join(CSRC, "rbf_attn_bench.cpp"), f"-L{PKG_DIR}", "-lrbfattn", "-Wl,-rpath,$ORIGIN",
+              "-o", tmp_bench])
+        shutil.copyfile(tmp_bench, BENCH_PATH + ".tmp")
+        os.chmod(BENCH_PATH + ".tmp", 0o755)
+        os.replace(BENCH_PATH + ".tmp", BENCH_PATH)
     if verbose:
-        print(f"built {LIB_PATH}", file=sys.stderr)
+        print(f"built {LIB_PATH} and {BENCH_PATH}", file=sys.stderr)
     return LIB_PATH
 
 

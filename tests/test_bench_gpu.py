@@ -45,6 +45,11 @@ def test_bench_json_line(cuda_device):
     assert r["cold"]["step_us_median"] > 0 and r["cold"]["reps"] == 3
     # the op-level step runs the same kernels plus Python dispatch and allocation
     assert r["op_step_us"] >= 0.9 * r["ms_per_step"] * 1e3
+    # the C++ harness times the same step through the C ABI without Python
+    nh = r["native_harness"]
+    assert "error" not in nh, nh
+    assert nh["workload"] == "c2_model_bf16" and nh["steps"] == 3 and nh["cold"]["reps"] == 3
+    assert 0.5 < nh["step_us"] / (r["ms_per_step"] * 1e3) < 2.0
     # the forward keeps out (B,H,N,D bf16) and L (B,H,N fp32) for backward
     expect = (32 * 8 * 516 * 64 * 2 + 32 * 8 * 516 * 4) / 2 ** 20
     assert r["peak_fwd_activation_mb"] == pytest.approx(expect, rel=0.05)
@@ -71,3 +76,7 @@ def test_bench_extra_configs(cuda_device):
         assert c["op_step_us"] >= 0.9 * c["step_us"]
         assert c["roofline"]["bound"] == "mfma"
         check_roofline(c["roofline"], c["step_kernels"])
+    # the C++ harness (C ABI, no Python) times the same C3 step
+    nh = r["c3"]["native_harness"]
+    assert "error" not in nh, nh
+    assert 0.8 < nh["step_us"] / r["c3"]["step_us"] < 1.25
