@@ -29,7 +29,8 @@ Timing protocol
   * `op_step_us`: the same step through the torch ops instead of the C ABI
     (run_triton_rbf / run_triton_non_softmax_rbf forward, then backward through
     their autograd): Python dispatch and the outputs, L and gradients from
-    torch's caching allocator on top of the same kernels.
+    torch's caching allocator on top of the same kernels.  `op_graph_step_us`:
+    those op-level steps captured ten to a graph and replayed (per step).
 """
 from __future__ import annotations
 
@@ -333,8 +334,25 @@ def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold
         for _ in range(max(3, warmup // 10)):
             op_step()
         ms_op = timer.loop(op_step, steps)
-    del oq, ok_, ov
     log(f"  op-level step (torch ops + autograd): {ms_op * 1e3:.2f} us")
+    ms_op_graph = None
+    if graph:
+        # The op-level steps captured in one graph (outputs and gradients from
+        # the graph's pool): the host cost of dispatch and autograd is paid
+        # once, at capture.
+        try:
+            og = torch.cuda.CUDAGraph()
+            oq.grad = ok_.grad = ov.grad = None
+            with torch.cuda.graph(og):
+                for _ in range(GRAPH_STEPS):
+                    op_step()
+            og.replay()
+            ms_op_graph = timer.loop(og.replay, max(1, steps // GRAPH_STEPS)) / GRAPH_STEPS
+            log(f"  op-level graph step: {ms_op_graph * 1e3:.2f} us ({GRAPH_STEPS} steps per graph)")
+            del og
+        except RuntimeError as e:  # reported as null; the eager measurements stand
+            log(f"  op-level graph step: capture failed ({e})")
+    del oq, ok_, ov
 
     # Per-kernel averages, each kernel in a loop of its own (events between
     # single launches add their own cost to every launch).  With a one-launch
@@ -365,6 +383,7 @@ def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold
         },
         "graph_step_us": round(ms_graph * 1e3, 3) if ms_graph is not None else None,
         "op_step_us": round(ms_op * 1e3, 3),
+        "op_graph_step_us": round(ms_op_graph * 1e3, 3) if ms_op_graph is not None else None,
         "kernel_us": {kk: round(t * 1e3, 3) for kk, t in kern_ms.items()},
         "step_kernels": list(step_kernels),
         "roofline": roofline(w, dom, per_pair[dom] * w.D * P, kern_ms[dom] * 1e-3, peak),
@@ -650,6 +669,7 @@ def main() -> int:
         "cold": head["cold"],
         "graph_step_us": head["graph_step_us"],
         "op_step_us": head["op_step_us"],
+        "op_graph_step_us": head["op_graph_step_us"],
         "kernel_us": head["kernel_us"],
         "step_kernels": head["step_kernels"],
         "roofline": head["roofline"],

@@ -45,6 +45,7 @@ def test_bench_json_line(cuda_device):
     assert r["cold"]["step_us_median"] > 0 and r["cold"]["reps"] == 3
     # the op-level step runs the same kernels plus Python dispatch and allocation
     assert r["op_step_us"] >= 0.9 * r["ms_per_step"] * 1e3
+    assert r["op_graph_step_us"] is not None and r["op_graph_step_us"] > 0
     # the C++ harness times the same step through the C ABI without Python
     nh = r["native_harness"]
     assert "error" not in nh, nh
