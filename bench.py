@@ -592,7 +592,10 @@ def native_harness(workload: str, steps: int, warmup: int, cold_reps: int, ramp_
         return {"error": f"{exe} not built (python -m rbf_attention_amd.build)"}
     cmd = [exe, "--workload", workload, "--steps", str(steps), "--warmup", str(warmup), "--cold-reps",
            str(cold_reps), "--ramp-seconds", str(ramp_s)]
-    p = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
+    try:
+        p = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
+    except subprocess.TimeoutExpired:
+        return {"error": "timed out after 120 s"}
     if p.returncode != 0:
         return {"error": f"rc={p.returncode}: {p.stderr.strip()[-500:]}"}
     return json.loads(p.stdout.strip().splitlines()[-1])
