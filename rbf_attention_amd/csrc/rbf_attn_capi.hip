@@ -112,12 +112,15 @@ rbf::Params make_params(const rbf_attn_args* a) {
   p.org = rem == 0 ? 0 : rem - 32;
   p.nblk = (a->N - p.org) / 32;
   // Heaviest-group-first chunks of heads on one XCD: as many heads as have
-  // 8 MB of streamed operands (K and V, or Q and dO) between them.  Measured
-  // on MI355X: short heads want the whole XCD share in one chunk (no heavy
-  // group left for the end of the launch), 4 MB heads want head-major order
-  // (their groups share K/V in L2 while they run together).
+  // 16 MB of streamed operands (K and V, or Q and dO) between them, rounded
+  // up.  Measured on MI355X (bf16, sums of the three streaming kernels):
+  // short heads want the whole XCD share in one chunk (no heavy group left
+  // for the end of the launch); 4.2 MB heads (N = 8196, D = 128) ran 1.3 %
+  // faster in chunks of 4 than of 1, and 6 or 8 were slower again; 8.4 MB
+  // heads 0.6 % faster in chunks of 2 than of 1; for 2 MB heads chunks of 4
+  // and 8 were within 0.5 %.
   const long long per_head = 2LL * a->N * a->D * (long long)elem_size(a->dtype);
-  const long long fit = per_head > 0 ? (8LL << 20) / per_head : 1;
+  const long long fit = per_head > 0 ? ((16LL << 20) + per_head - 1) / per_head : 1;
   const long long per_xcd = ((long long)a->B * a->H) / 8;
   p.hchunk = (int)(fit < 1 ? 1 : (fit > per_xcd ? (per_xcd > 0 ? per_xcd : 1) : fit));
   // RBF_ATTN_HCHUNK overrides the chunk size (tuning sweeps).
