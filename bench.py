@@ -601,6 +601,46 @@ def native_harness(workload: str, steps: int, warmup: int, cold_reps: int, ramp_
     return json.loads(p.stdout.strip().splitlines()[-1])
 
 
+# Length sweep (--length-sweep): bf16 causal softmax, the same 2^19 tokens per
+# step at every N (B x H x N = 524288, H = 8 or 16), so that the step's kernels
+# move from the head-resident range to long sequences at a fixed token count.
+SWEEP_N = (516, 1028, 2052, 4100, 8196, 16388)
+
+
+def length_sweep(dev, timer) -> dict:
+    """C-ABI fwd+bwd TFLOP/s (14 D P flops per step, the headline formula)
+    over SWEEP_N for D = 64 and D = 128."""
+    import torch
+
+    from rbf_attention_amd import _lib
+    from rbf_attention_amd import workloads as wl
+
+    rows = []
+    for D, H in ((64, 8), (128, 16)):
+        for N in SWEEP_N:
+            B = max(1, (1 << 19) // (H * N))
+            w = wl.Workload(f"sweep_d{D}_n{N}", B=B, H=H, content=N - 4, D=D, dtype="bf16", key_lognormal=0.5)
+            bufs, a = setup_workload(w, dev)
+            sp = timer.stream.cuda_stream
+
+            def step():
+                _lib.call("rbf_attn_fwd", a, sp)
+                _lib.call("rbf_attn_bwd", a, sp)
+
+            timer.ramp(step, 0.1)
+            n = max(3, min(50, int(0.05 / max(w.flops_fwd_bwd() / 700e12, 1e-6))))
+            ms = timer.loop(step, n)
+            tf = w.flops_fwd_bwd() / (ms * 1e-3) / 1e12
+            rows.append({"D": D, "N": N, "B": B, "H": H, "step_us": round(ms * 1e3, 2), "tflops": round(tf, 1),
+                         "pct_of_bf16_peak": round(100 * tf / PEAK_TFLOPS["bf16"], 2),
+                         "bwd_kernels": _lib.bwd_kernels(a)})
+            log(f"  D={D} N={N} B={B} H={H}: {ms * 1e3:.1f} us, {tf:.0f} TFLOP/s")
+            del bufs
+            torch.cuda.empty_cache()
+    return {"config": {"dtype": "bf16", "causal": True, "softmax": True, "tokens_per_step": 1 << 19,
+                       "gamma": "1/(2 sqrt(D))"}, "rows": rows}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -620,6 +660,8 @@ def main() -> int:
     ap.add_argument("--no-extra-configs", action="store_true", help="skip the C3/C4 objects")
     ap.add_argument("--no-ref-sweep", action="store_true", help="skip the reference's own fp16 length sweep")
     ap.add_argument("--no-native", action="store_true", help="skip the C++ harness (rbf_attn_bench) timings")
+    ap.add_argument("--length-sweep", action="store_true",
+                    help="add a bf16 fwd+bwd TFLOP/s sweep over N (D = 64 and 128, fixed tokens per step)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="run one device copy of this many MiB before timing (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -706,6 +748,9 @@ def main() -> int:
         log("decode (KV cache) ...")
         result["decode"] = decode_bench(dev, 50)
         log(f"  {result['decode']['value']} GB/s, {result['decode']['us_per_call']} us/call")
+    if args.length_sweep:
+        log("length sweep ...")
+        result["length_sweep"] = length_sweep(dev, timer)
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)

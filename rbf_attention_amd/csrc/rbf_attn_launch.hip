@@ -251,6 +251,11 @@ hipError_t dq_default(const Params& p, hipStream_t st) {
     return bins_fit(p) ? dq_cfg<DP, SM, 4, 1, 128, true, true>(p, st) : dq_cfg<DP, SM, 4, 1, 128>(p, st);
   }
   else {
+    // Short heads: 4-wave work-groups over 32-key register-staged tiles,
+    // K^T read next to the dQ MFMAs.  Measured against the 8-wave LDS-DMA
+    // form (bf16 softmax dQ): B63 H16 N516 302 -> 258 us, B8 H16 N516 36.5 ->
+    // 33.2, B31 H16 N1028 363 -> 344; slower from N = 1500 (73 -> 80).
+    if (p.N < 1200) return dq_cfg<DP, SM, 4, 1, 32, false>(p, st);
     if (use_dma(p, DP))
       return bins_fit(p) ? dq_cfg<DP, SM, 8, 1, 64, true, true, true>(p, st) : dq_cfg<DP, SM, 8, 1, 64, true, false, true>(p, st);
     return bins_fit(p) ? dq_cfg<DP, SM, 8, 1, 32, true, true>(p, st) : dq_cfg<DP, SM, 8, 1, 32>(p, st);
@@ -280,11 +285,13 @@ hipError_t dkdv_default(const Params& p, hipStream_t st) {
     return bins_fit(p) ? dkdv_cfg<DP, SM, 4, 1, 128, false, false, false, true>(p, st)
                        : dkdv_cfg<DP, SM, 4, 1, 128, false>(p, st);
   } else {
-    // the long-sequence paired kernel measured slower with the bin loop
-    // (LDS-DMA for long sequences only: the two-pair binned form spills with it)
-    if (p.N >= kLongSeq)
-      return use_dma(p, DP) ? dkdv_pair_cfg<DP, SM, 4, 64, true, false, true>(p, st) : dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st);
-    return bins_fit(p) ? dkdv_pair_cfg<DP, SM, 2, 64, false, true>(p, st) : dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
+    // Four key blocks per work-group, one group each (no bin loop), at every
+    // length; LDS-DMA from N = 1024.  Measured against the binned two-block
+    // form (bf16 softmax dK/dV): B32 H8 N516 156 -> 114 us, B63 H16 N516 657
+    // -> 470, B31 H16 N1028 891 -> 562 (DMA; 585 without), B4 H16 N1500 193
+    // -> 114; at B2 H8 N300 18.5 against 18.8.
+    if (p.N >= 1024 && use_dma(p, DP)) return dkdv_pair_cfg<DP, SM, 4, 64, true, false, true>(p, st);
+    return dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st);
   }
 }
 
