@@ -218,11 +218,14 @@ hipError_t fwd_default(const Params& p, hipStream_t st) {
   }
   if constexpr (kIsF32) return fwd_cfg<DP, SM, 4, 32>(p, st);
   else if constexpr (DP <= 64) {
-    if (DP == 64 && use_dma(p, DP)) {
-      if (p.N >= kLongSeq)
-        return bins_fit(p) ? fwd_cfg<DP, SM, 8, 128, true, true>(p, st) : fwd_cfg<DP, SM, 8, 128, false, true>(p, st);
-      return bins_fit(p) ? fwd_cfg<DP, SM, 4, 64, true, true>(p, st) : fwd_cfg<DP, SM, 4, 64, false, true>(p, st);
-    }
+    // LDS-DMA: 4 waves over 64-key tiles at every length, one group per
+    // work-group.  The bin loop re-primes the three-tile pipeline for each of
+    // its groups with nothing to overlap it; separate work-groups overlap one
+    // another's.  Measured against the binned forms (bf16 softmax fwd, us):
+    // B63 H8 N1028 149 -> 131, B20 H8 N700 30.4 -> 27.9, B16 H8 N2052 118 ->
+    // 108, B15 H8 N4100 382 -> 344, B4 H8 N8196 354 -> 346 (8 waves over
+    // 128-key tiles: 374 and 358); B16 H8 N1028 37.8 -> 39.4.
+    if (DP == 64 && use_dma(p, DP)) return fwd_cfg<DP, SM, 4, 64, false, true>(p, st);
     if (p.N >= kLongSeq) return bins_fit(p) ? fwd_cfg<DP, SM, 8, 128, true>(p, st) : fwd_cfg<DP, SM, 8, 128>(p, st);
     return bins_fit(p) ? fwd_cfg<DP, SM, 4, 64, true>(p, st) : fwd_cfg<DP, SM, 4, 64>(p, st);
   } else {
@@ -245,9 +248,11 @@ hipError_t dq_default(const Params& p, hipStream_t st) {
   if constexpr (kIsF32) return dq_cfg<DP, SM, 4, 1, 32>(p, st);
   else if constexpr (DP <= 64) {
     // (LDS-DMA on 64-key tiles: three 128-key tiles leave room for one
-    // four-wave work-group per CU)
-    if (DP == 64 && use_dma(p, DP))
-      return bins_fit(p) ? dq_cfg<DP, SM, 4, 1, 64, true, true, true>(p, st) : dq_cfg<DP, SM, 4, 1, 64, true, false, true>(p, st);
+    // four-wave work-group per CU.)  One group per work-group, as for the
+    // forward: against the binned form (bf16 softmax dQ, us) B63 H8 N1028 192
+    // -> 168, B16 H8 N1028 45.0 -> 43.2, B20 H8 N700 33.5 -> 31.4, B16 H8
+    // N2052 140 -> 126, B15 H8 N4100 491 -> 419, B4 H8 N8196 450 -> 414.
+    if (DP == 64 && use_dma(p, DP)) return dq_cfg<DP, SM, 4, 1, 64, true, false, true>(p, st);
     return bins_fit(p) ? dq_cfg<DP, SM, 4, 1, 128, true, true>(p, st) : dq_cfg<DP, SM, 4, 1, 128>(p, st);
   }
   else {
@@ -308,6 +313,13 @@ hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
     case 3: return fwd_cfg<DP, SM, 4, 128>(p, st);
     case 4: return fwd_cfg<DP, SM, 2, 64>(p, st);
     case 5: return fwd_cfg<DP, SM, 4, 32>(p, st);
+    case 6:
+      if (use_dma(p, DP)) return fwd_cfg<DP, SM, 4, 64, false, true>(p, st);
+      break;
+    case 7: return fwd_cfg<DP, SM, 4, 64, true>(p, st);
+    case 8:
+      if (use_dma(p, DP)) return fwd_cfg<DP, SM, 8, DP == 64 ? 128 : 64, false, true>(p, st);
+      break;
     case 10:
       if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return hr_fwd(p, SM, 8, st); }
       break;
@@ -331,6 +343,9 @@ hipError_t dq_any_cfg(const Params& p, hipStream_t st) {
       case 9: return dq_cfg<DP, SM, 4, 1, 32, false>(p, st);
       case 10: return dq_cfg<DP, SM, 8, 1, 32>(p, st);
       case 11: return dq_cfg<DP, SM, 8, 1, 32, false>(p, st);
+      case 14:
+        if (use_dma(p, DP)) return dq_cfg<DP, SM, 8, 1, 64, true, false, true>(p, st);
+        break;
       default: break;
     }
   }
@@ -346,6 +361,10 @@ hipError_t dq_any_cfg(const Params& p, hipStream_t st) {
     case 6: return dq_cfg<DP, SM, 4, 1, 64, false>(p, st);
     case 8: return dq_cfg<DP, SM, 4, 1, 128>(p, st);
     case 11: return dq_cfg<DP, SM, 8, 1, 64>(p, st);
+    case 12:
+      if (use_dma(p, DP)) return dq_cfg<DP, SM, 4, 1, 64, true, false, true>(p, st);
+      break;
+    case 13: return dq_cfg<DP, SM, 4, 1, 64, true, true>(p, st);
     default: break;
   }
   }
