@@ -281,10 +281,11 @@ hipError_t dkdv_default(const Params& p, hipStream_t st) {
   if constexpr (kIsF32) return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
   else if constexpr (DP <= 64) {
     // LDS-DMA from N = 4096 on: at N = 512-2048 the D = 64 dK/dV measured as
-    // fast or slower with it (C4 188 -> 191 us), at N = 8192 faster (605 -> 589)
+    // fast or slower with it (C4 188 -> 191 us), at N = 8192 faster (605 -> 589).
+    // With it, one group per work-group (as the forward and dQ): 0.7-3.4 %
+    // faster than the binned form at B15 H8 N4100, B4 H8 N8196, B2 H8 N16388.
     if (DP == 64 && p.N >= 2 * kLongSeq && use_dma(p, DP))
-      return bins_fit(p) ? dkdv_cfg<DP, SM, 8, 1, 128, true, false, false, true, true>(p, st)
-                         : dkdv_cfg<DP, SM, 8, 1, 128, true, false, false, false, true>(p, st);
+      return dkdv_cfg<DP, SM, 8, 1, 128, true, false, false, false, true>(p, st);
     if (p.N >= kLongSeq)
       return bins_fit(p) ? dkdv_cfg<DP, SM, 8, 1, 128, true, false, false, true>(p, st) : dkdv_cfg<DP, SM, 8, 1, 128>(p, st);
     return bins_fit(p) ? dkdv_cfg<DP, SM, 4, 1, 128, false, false, false, true>(p, st)
