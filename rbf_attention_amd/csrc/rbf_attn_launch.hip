@@ -226,8 +226,13 @@ hipError_t fwd_default(const Params& p, hipStream_t st) {
     // 108, B15 H8 N4100 382 -> 344, B4 H8 N8196 354 -> 346 (8 waves over
     // 128-key tiles: 374 and 358); B16 H8 N1028 37.8 -> 39.4.
     if (DP == 64 && use_dma(p, DP)) return fwd_cfg<DP, SM, 4, 64, false, true>(p, st);
-    if (p.N >= kLongSeq) return bins_fit(p) ? fwd_cfg<DP, SM, 8, 128, true>(p, st) : fwd_cfg<DP, SM, 8, 128>(p, st);
-    return bins_fit(p) ? fwd_cfg<DP, SM, 4, 64, true>(p, st) : fwd_cfg<DP, SM, 4, 64>(p, st);
+    // Register staging (padded head dims, or strides past the DMA range): one
+    // group per work-group, 4 waves over 64-key tiles up to N = 8192.
+    // Measured against the binned forms at D = 48 (bf16 softmax fwd, us): B63
+    // H8 N1028 149 -> 117, B20 H8 N700 26.9 -> 23.5, B16 H8 N2052 111 -> 103;
+    // at B4 H8 N8196 the binned 8-wave form stays ahead (360 against 366).
+    if (p.N >= 4 * kLongSeq) return bins_fit(p) ? fwd_cfg<DP, SM, 8, 128, true>(p, st) : fwd_cfg<DP, SM, 8, 128>(p, st);
+    return fwd_cfg<DP, SM, 4, 64>(p, st);
   } else {
     if (use_dma(p, DP)) return bins_fit(p) ? fwd_cfg<DP, SM, 8, 64, true, true>(p, st) : fwd_cfg<DP, SM, 8, 64, false, true>(p, st);
     return bins_fit(p) ? fwd_cfg<DP, SM, 8, 64, true>(p, st) : fwd_cfg<DP, SM, 8, 64>(p, st);
@@ -253,7 +258,9 @@ hipError_t dq_default(const Params& p, hipStream_t st) {
     // -> 168, B16 H8 N1028 45.0 -> 43.2, B20 H8 N700 33.5 -> 31.4, B16 H8
     // N2052 140 -> 126, B15 H8 N4100 491 -> 419, B4 H8 N8196 450 -> 414.
     if (DP == 64 && use_dma(p, DP)) return dq_cfg<DP, SM, 4, 1, 64, true, false, true>(p, st);
-    return bins_fit(p) ? dq_cfg<DP, SM, 4, 1, 128, true, true>(p, st) : dq_cfg<DP, SM, 4, 1, 128>(p, st);
+    // register staging: one group per work-group (D = 48: 1.0-4.7 % faster
+    // than binned at N = 700-8196)
+    return dq_cfg<DP, SM, 4, 1, 128>(p, st);
   }
   else {
     // Short heads: 4-wave work-groups over 32-key register-staged tiles,
@@ -286,10 +293,12 @@ hipError_t dkdv_default(const Params& p, hipStream_t st) {
     // faster than the binned form at B15 H8 N4100, B4 H8 N8196, B2 H8 N16388.
     if (DP == 64 && p.N >= 2 * kLongSeq && use_dma(p, DP))
       return dkdv_cfg<DP, SM, 8, 1, 128, true, false, false, false, true>(p, st);
-    if (p.N >= kLongSeq)
-      return bins_fit(p) ? dkdv_cfg<DP, SM, 8, 1, 128, true, false, false, true>(p, st) : dkdv_cfg<DP, SM, 8, 1, 128>(p, st);
-    return bins_fit(p) ? dkdv_cfg<DP, SM, 4, 1, 128, false, false, false, true>(p, st)
-                       : dkdv_cfg<DP, SM, 4, 1, 128, false>(p, st);
+    // Register staging: one group per work-group, 4 waves below N = 4096 and 8
+    // above.  Against the binned forms at D = 48 (bf16 softmax dK/dV, us): B63
+    // H8 N1028 208 -> 200, B20 H8 N700 38.1 -> 35.9, B16 H8 N2052 169 -> 160,
+    // B4 H8 N8196 536 -> 528.
+    if (p.N >= 2 * kLongSeq) return dkdv_cfg<DP, SM, 8, 1, 128>(p, st);
+    return dkdv_cfg<DP, SM, 4, 1, 128, false>(p, st);
   } else {
     // Four key blocks per work-group, one group each (no bin loop), at every
     // length; LDS-DMA from N = 1024.  Measured against the binned two-block
