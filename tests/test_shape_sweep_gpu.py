@@ -5,7 +5,7 @@ dispatch boundaries, each checked to the bounds of test_parity_gpu:
   * paired dK/dV kernel at D = 128, with LDS-DMA tile staging from
     N = 2048 and register staging below (D = 128 exactly; padded head dims
     such as 96 or 120 always stage through registers);
-  * D = 64 forward with LDS-DMA from N = 2048, dK/dV from N = 4096;
+  * D = 64 forward and dQ with LDS-DMA at every length, dK/dV from N = 4096;
   * head dims padded to 32 / 64 / 128 (24, 40, 96, 120);
   * B*H not a multiple of 8 (no per-XCD head chunks), B*H = 1;
   * num_prefix register tokens, non-causal masks, fp16 and fp32.
