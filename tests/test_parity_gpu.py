@@ -24,12 +24,17 @@ reference kernels' own roundings make unavoidable):
     realization of that rounding against another differs by up to ~1.4x (a
     CPU backward fed the kernel's own O and L reproduces its dK exactly, and
     the kernel's per-row O and Delta errors are distributed as the model's).
-  * A reference that is identically zero (dQ for N = 1: one visible key,
-    dS = 0) is checked with max-abs <= 1e-5 instead of a relative norm.
+  * A reference that is zero or numerically zero, every entry below 1e-5
+    next to inputs of order 1 (dQ for N = 1: one visible key, dS = 0; for
+    N = 2 with a nearly one-hot P: ~4e-7), is checked with max-abs <= 1e-5
+    instead of a relative norm, which there measures only rounding noise.
   * dQ and dK at N <= 2 are checked at rel-L2 <= 3e-2: with one or two
     visible keys they are proportional to a single dS_ij, and Delta_i = rowsum(O * dO) is
     taken from the bf16 output as in the reference kernel
     (rbf_attention.py:275-276), whose rounding then sets the relative error.
+  * Where the rounding model itself misses the rel-L2 bound (dQ of a
+    handful of visible keys, e.g. N = 6 in fp16: 1.86e-2), the kernel's
+    rel-L2 may not exceed 1.2x the model's, whatever the tensor's size.
 Big configurations are compared on sampled (b, h) slices -- every slice is an
 independent problem -- plus size-independent properties at full size.
 Set RBF_PARITY_LOG=<file> to append every comparison's metrics as JSON lines.
@@ -102,10 +107,14 @@ def check(name, got, ref, dtype, rel_l2_max=1e-2, kind=None, model=None, model_r
     if dtype == torch.float32:
         assert e["max_abs"] <= 1e-4, info
         return
-    if not np.linalg.norm(ref) > 0:
+    if not e["max_ref"] >= 1e-5:
         assert e["max_abs"] <= 1e-5, info
         return
-    assert e["rel_l2"] <= rel_l2_max, info
+    rel_max = rel_l2_max
+    if m is not None and m["rel_l2"] > rel_l2_max:
+        # the reference's own arithmetic misses the bound: the kernel may not do worse
+        rel_max = MODEL_RATIO * m["rel_l2"]
+    assert e["rel_l2"] <= rel_max, info
     if elementwise:
         allowed = 0 if m is None else math.ceil(1.25 * m["n_viol"])
         assert e["n_viol"] <= allowed, info

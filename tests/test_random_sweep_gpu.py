@@ -1,0 +1,80 @@
+"""Seeded random shapes against the float64 oracle, to the bounds of
+test_parity_gpu (rel-L2, elementwise O/dV, tensor-wide dQ/dK, rounding-model
+ratio).
+
+The fixed parity tests pick one dimension at a time (head dims at N = 77,
+ragged N at D = 64, masks at one shape, ...).  These cases draw every
+dimension at once from one fixed generator, so that combinations the fixed
+tests leave out (a padded head dim with a long prefix, fp16 with a
+non-causal mask at a ragged length, strided inputs with D = 24, ...) run
+through whichever kernels the launchers pick for them.  Sizes stay where the
+oracle finishes in about a second (N <= 2000, B * H <= 9).
+
+Inputs are contiguous (B, H, N, D) tensors or (B, H, N, D) views of
+token-major (B, N, H, D) storage, the layout a model's QKV projection
+produces."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from test_parity_gpu import compare_case, rand_inputs
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+DT_NAMES = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}
+
+
+def draw_cases(n, seed=20261202):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        D = 8 * int(rng.integers(1, 17))
+        # log-uniform over 1..2000 (ragged short heads), or uniform over 500..2000
+        N = int(np.exp(rng.uniform(0.0, math.log(2000.0)))) if rng.random() < 0.6 else int(rng.integers(500, 2001))
+        B = int(rng.integers(1, 4))
+        H = int(rng.integers(1, 4))
+        dtype = DTYPES[int(rng.choice(3, p=[0.55, 0.3, 0.15]))]
+        softmax = bool(rng.random() < 0.6)
+        causal = bool(rng.random() < 0.75)
+        num_prefix = 0 if rng.random() < 0.6 else int(rng.integers(1, min(N, 64) + 1))
+        gamma = float(rng.choice([1.0 / math.sqrt(D), 0.5 / math.sqrt(D), rng.uniform(0.02, 0.3)]))
+        token_major = bool(rng.random() < 0.35)
+        cases.append((i, B, H, N, D, dtype, softmax, causal, num_prefix, gamma, token_major))
+    return cases
+
+
+CASES = draw_cases(64)
+
+
+def case_id(c):
+    i, B, H, N, D, dtype, softmax, causal, npre, gamma, tm = c
+    return (f"r{i}_B{B}H{H}N{N}D{D}_{DT_NAMES[dtype]}_{'sm' if softmax else 'ns'}_"
+            f"{'causal' if causal else 'full'}_p{npre}{'_tm' if tm else ''}")
+
+
+def test_draw_covers_the_dispatch_space():
+    """The fixed draw reaches every dtype, both variants, both masks, prefixes,
+    strided inputs, each head-dim padding class (<= 32, <= 64, <= 128), and
+    lengths from below one 64-token tile to past 1200 tokens (where the D = 128
+    dQ switches kernels)."""
+    assert {c[5] for c in CASES} == set(DTYPES)
+    assert {c[6] for c in CASES} == {True, False}
+    assert {c[7] for c in CASES} == {True, False}
+    assert any(c[8] > 0 for c in CASES) and any(c[10] for c in CASES)
+    assert {(c[4] > 32) + (c[4] > 64) for c in CASES} == {0, 1, 2}
+    assert min(c[3] for c in CASES) < 64 and max(c[3] for c in CASES) > 1200
+
+
+@pytest.mark.parametrize("case", CASES, ids=case_id)
+def test_random_shape(cuda_device, case):
+    i, B, H, N, D, dtype, softmax, causal, npre, gamma, token_major = case
+    q, k, v, do = rand_inputs(B, H, N, D, dtype, cuda_device, std=1.0 if softmax else 0.5, seed=1000 + i,
+                              key_scale=0.5 if softmax else 0.0)
+    if token_major:
+        # same values, (B, H, N, D) views of (B, N, H, D) storage
+        q, k, v, do = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v, do))
+        assert q.stride(2) == H * D
+    compare_case(q, k, v, do, softmax=softmax, causal=causal, gamma=gamma, num_prefix=npre, tag=case_id(case))
