@@ -95,3 +95,59 @@ def test_decode_strided_cache_views(cuda_device):
     vb = torch.randn(B, L, H, D, generator=g).to(torch.bfloat16).to(cuda_device)
     q = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16).to(cuda_device)
     run_case(q, kb.transpose(1, 2), vb.transpose(1, 2), True, 0.0625, tag="strided")
+
+
+def draw_decode_cases(n, seed=16384):
+    """Every dimension of a decode call drawn at once from one fixed generator
+    (B, H, the query block T, cache length L, D, dtype, variant, gamma,
+    per-batch lengths, head-interleaved cache views)."""
+    rng = np.random.default_rng(seed)
+    dtypes = (torch.bfloat16, torch.float16, torch.float32)
+    cases = []
+    for i in range(n):
+        B = int(rng.integers(1, 5))
+        H = int(rng.integers(1, 5))
+        T = int(rng.choice([1, 1, 2, int(rng.integers(1, 33))]))
+        L = int(np.exp(rng.uniform(np.log(max(T, 2)), np.log(6000.0))))
+        L = max(L, T)
+        D = 8 * int(rng.integers(1, 17))
+        dtype = dtypes[int(rng.choice(3, p=[0.55, 0.3, 0.15]))]
+        softmax = bool(rng.random() < 0.65)
+        gamma = float(rng.choice([1.0 / D ** 0.5, 0.5 / D ** 0.5, rng.uniform(0.02, 0.3)]))
+        lens = [int(rng.integers(T, L + 1)) for _ in range(B)] if rng.random() < 0.4 else None
+        strided = bool(rng.random() < 0.35)
+        cases.append((i, B, H, T, L, D, dtype, softmax, gamma, lens, strided))
+    return cases
+
+
+DECODE_CASES = draw_decode_cases(24)
+
+
+def decode_id(c):
+    i, B, H, T, L, D, dtype, softmax, gamma, lens, strided = c
+    return (f"d{i}_B{B}H{H}T{T}L{L}D{D}_{str(dtype).split('.')[-1]}_{'sm' if softmax else 'ns'}"
+            f"{'_ragged' if lens else ''}{'_strided' if strided else ''}")
+
+
+def test_decode_draw_coverage():
+    """The draw reaches every dtype, both variants, single-token and block
+    queries, ragged lengths, strided caches and caches past 4096 tokens."""
+    assert {c[6] for c in DECODE_CASES} == {torch.bfloat16, torch.float16, torch.float32}
+    assert {c[7] for c in DECODE_CASES} == {True, False}
+    assert any(c[3] == 1 for c in DECODE_CASES) and any(c[3] > 4 for c in DECODE_CASES)
+    assert any(c[9] for c in DECODE_CASES) and any(c[10] for c in DECODE_CASES)
+    assert max(c[4] for c in DECODE_CASES) > 4096
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=decode_id)
+def test_decode_random(cuda_device, case):
+    i, B, H, T, L, D, dtype, softmax, gamma, lens, strided = case
+    std = 1.0 if softmax else 0.5
+    if strided:
+        g = torch.Generator().manual_seed(500 + i)
+        q = (torch.randn(B, H, T, D, generator=g) * std).to(dtype).to(cuda_device)
+        k = (torch.randn(B, L, H, D, generator=g) * std).to(dtype).to(cuda_device).transpose(1, 2)
+        v = torch.randn(B, L, H, D, generator=g).to(dtype).to(cuda_device).transpose(1, 2)
+    else:
+        q, k, v = make(B, H, T, L, D, dtype, cuda_device, seed=500 + i, std=std)
+    run_case(q, k, v, softmax, gamma, lens=lens, tag=decode_id(case))
