@@ -183,3 +183,98 @@ def test_pos_streaming_against_oracle(cuda_device, B, H, N, D, dtype, softmax, s
         dP = (dq + dk).sum(axis=0, keepdims=True) if shared else dq + dk
         check(f"{name0} dP h{h}", pp.grad[:, h:h + 1], dP, dtype)
     assert np.isfinite(np64(pp.grad)).all()
+
+
+def draw_fused_cases(n, seed=1688):
+    """The fused path's whole range, every dimension drawn at once: 16-bit,
+    32 < D <= 64, N <= 576 (the head-resident kernels take a term at any
+    number of heads), a term shared by the batch or one per entry, both
+    variants, masks, register prefixes, gamma, token-major output."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        D = 8 * int(rng.integers(5, 9))
+        # log-uniform over 1..576, or uniform over the longest heads 400..576
+        N = int(np.exp(rng.uniform(0.0, np.log(576.0)))) if rng.random() < 0.5 else int(rng.integers(400, 577))
+        if rng.random() < 0.4:  # at least one head per CU, as at the model's shape
+            B, H = int(rng.integers(16, 41)), 16
+        else:
+            B, H = int(rng.integers(1, 41)), int(rng.choice([1, 2, 4, 8]))
+        dtype = (torch.bfloat16, torch.float16)[int(rng.random() < 0.35)]
+        softmax = bool(rng.random() < 0.6)
+        causal = bool(rng.random() < 0.8)
+        npre = 0 if rng.random() < 0.5 else int(rng.integers(1, min(N, 64) + 1))
+        gamma = float(rng.choice([1.0 / math.sqrt(D), 0.5 / math.sqrt(D), rng.uniform(0.02, 0.2)]))
+        shared = bool(rng.random() < 0.6)
+        token_major = bool(rng.random() < 0.35)
+        cases.append((i, B, H, N, D, dtype, softmax, causal, npre, gamma, shared, token_major))
+    return cases
+
+
+FUSED_CASES = draw_fused_cases(16)
+
+
+def fused_id(c):
+    i, B, H, N, D, dtype, softmax, causal, npre, gamma, shared, tm = c
+    return (f"f{i}_B{B}H{H}N{N}D{D}_{str(dtype)[6:]}_{'sm' if softmax else 'ns'}_{'causal' if causal else 'full'}"
+            f"_p{npre}_{'shared' if shared else 'perbatch'}{'_tm' if tm else ''}")
+
+
+def test_fused_draw_coverage():
+    """The draw spans fewer and more heads than the 256 CUs, both variants,
+    both kinds of term, short and long heads and token-major output."""
+    heads = [c[1] * c[2] for c in FUSED_CASES]
+    assert min(heads) < 256 <= max(heads)
+    assert {c[6] for c in FUSED_CASES} == {True, False} and {c[10] for c in FUSED_CASES} == {True, False}
+    assert min(c[3] for c in FUSED_CASES) < 64 and max(c[3] for c in FUSED_CASES) > 448
+    assert any(c[11] for c in FUSED_CASES) and any(c[8] for c in FUSED_CASES)
+
+
+@pytest.mark.parametrize("case", FUSED_CASES, ids=fused_id)
+def test_fused_pos_random_against_oracle(cuda_device, case):
+    """The fused term against the float64 oracle on the rounded sums
+    (q + P, k + P): O, dQ, dK, dV on the first and last (b, h) slices, and the
+    term's gradient on the last head (sum over the batch for a shared term)."""
+    import numpy as np
+
+    from oracle import rbf_oracle as ro
+    from test_parity_gpu import check, np64
+
+    i, B, H, N, D, dtype, softmax, causal, npre, gamma, shared, token_major = case
+    q, k, v, do, P = inputs(B, H, N, D, dtype, cuda_device, seed=4000 + i, shared=shared)
+    if not softmax:  # keep the unnormalised weights away from underflow
+        q, k, P = q * 0.5, k * 0.5, P * 0.5
+    a = _lib.Args()
+    a.abi_version, a.variant, a.dtype = _lib.ABI_VERSION, 0 if softmax else 1, _lib.DTYPE_CODES[dtype]
+    a.B, a.H, a.N, a.D, a.causal, a.gamma = B, H, N, D, int(causal), gamma
+    assert _lib.pos_supported(a)
+    fn = ra.run_triton_rbf if softmax else ra.run_triton_non_softmax_rbf
+    qq, kk, vv, pp = (x.clone().requires_grad_(True) for x in (q, k, v, P))
+    print(f"case {fused_id(case)} gamma={gamma:.4f}", flush=True)
+    out = fn(qq, kk, vv, causal, sm_scale=gamma, num_prefix=npre, pos=pp, token_major=token_major)
+    out.backward(do)
+    torch.cuda.synchronize()
+    if token_major:  # (B, H, N, D) view of (B, N, H, D) storage
+        assert out.shape == (B, H, N, D) and out.transpose(1, 2).is_contiguous()
+    qs, ks = q + P, k + P  # rounded to the element type, as separate adds store them
+    fwd = ro.softmax_forward if softmax else ro.non_softmax_forward
+    bwd = ro.softmax_backward if softmax else ro.non_softmax_backward
+    r = ro.rounder("bf16" if dtype == torch.bfloat16 else "fp16")
+    for b, h in ((0, 0), (B - 1, H - 1)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        arr = [np64(x)[sl] for x in (qs, ks, v, do)]
+        O = fwd(arr[0], arr[1], arr[2], gamma, causal, npre)
+        O = O[0] if softmax else O
+        grads = bwd(*arr, gamma, causal, npre)
+        model = ro.rounded_model(*arr, gamma, softmax=softmax, causal=causal, num_prefix=npre, rnd=r, out_rnd=r)
+        for j, (name, got, ref) in enumerate(zip(("O", "dQ", "dK", "dV"), (out, qq.grad, kk.grad, vv.grad),
+                                                 (O,) + tuple(grads))):
+            check(f"{fused_id(case)} b{b}h{h} {name}", got[sl], ref, dtype, kind=name, model=model[j])
+    h = H - 1
+    arr = [np64(x)[:, h:h + 1] for x in (qs, ks, v, do)]
+    dq, dk, _ = bwd(*arr, gamma, causal, npre)
+    dP = (dq + dk).sum(axis=0, keepdims=True) if shared else dq + dk
+    check(f"{fused_id(case)} dP h{h}", pp.grad[:, h:h + 1], dP, dtype)
+    assert np.isfinite(np64(pp.grad)).all()
