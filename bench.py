@@ -19,10 +19,19 @@ Timing protocol
   * `value` / `ms_per_step`: exactly K back-to-back steps between two HIP
     events on the launch stream (warm caches: the step's ~205 MB working set
     stays in the 256 MB MALL between steps).
-  * `cold`: the median over reps of one step timed alone after a 512 MiB
-    write that evicts L2 and MALL (outside the events).
-  * `kernel_us`: each kernel of the step in an event-timed loop of its own;
-    the roofline entry is computed from the dominant one.
+  * `kernel_us`: each kernel of the step in an event-timed loop of its own,
+    run right after the step loop (clocks still at their steady state), of
+    at least 200 launches and 0.2 s; the roofline entry is computed from the
+    dominant one.  `kernel_sum_us` is the sum over the step's kernels, which
+    should match `step_us` (the kernels of a step run back to back).
+  * `cold`: the protocol of the reference's do_bench (a cache-evicting write
+    before every rep; rbf_attention.py:1877, 1888): the median over >= 20
+    reps of one step timed alone after a 512 MiB write that evicts L2 and
+    MALL (outside the events); likewise the forward alone, the backward alone
+    from the saved forward outputs, and each kernel of the step.  `value` is
+    the warm step: in a model the attention's inputs are written by the
+    projections just before it (and dO by the layer above), so they arrive
+    in the cache hierarchy as they do in back-to-back steps.
   * `native_harness`: the same step timed by rbf_attn_bench, a C++ program
     that calls the C ABI directly (no Python), in a child process, with the
     same protocol (ramp, warm-up, K steps between events, cold reps).
@@ -194,6 +203,13 @@ class Timer:
         self.torch, self.dev, self.stream = torch, dev, stream
         self._flush = None
 
+    def kernel_loop(self, fn, min_s: float = 0.2, min_n: int = 200) -> float:
+        """Mean ms of back-to-back calls of one kernel: at least min_n calls
+        and min_s seconds, after a short loop that also estimates the count."""
+        est = self.loop(fn, 20)
+        n = max(min_n, int(math.ceil(min_s / max(est * 1e-3, 1e-7))))
+        return self.loop(fn, min(n, 20000))
+
     def loop(self, fn, n: int) -> float:
         """Mean ms of n back-to-back calls between two events."""
         torch = self.torch
@@ -292,9 +308,31 @@ def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold
     wall = time.perf_counter() - wall0
     log(f"{w.name}: step {ms_step * 1e3:.2f} us over {steps} steps (ramp {ramp_n} steps, wall {wall:.3f} s)")
 
+    # Per-kernel averages, each kernel in a loop of its own (events between
+    # single launches add their own cost to every launch), right after the
+    # step loop while the clocks are at their steady state.  With a
+    # one-launch backward its two stages are timed too, for reference.
+    bwd_launches = _lib.bwd_kernels(a)
+    step_kernels = ("fwd", "bwd") if bwd_launches == 1 else ("fwd", "bwd_dq", "bwd_dkdv")
+    calls = {"fwd": fwd, "bwd": bwd, "bwd_dq": stage(1), "bwd_dkdv": stage(2)}
+    timed_kernels = step_kernels + (("bwd_dq", "bwd_dkdv") if bwd_launches == 1 else ())
+    kern_ms = {kname: timer.kernel_loop(calls[kname]) for kname in timed_kernels}
+    for kname, t in kern_ms.items():
+        log(f"  {kname}: {t * 1e3:.2f} us/launch" + ("" if kname in step_kernels else " (stage alone)"))
+    kern_sum = sum(kern_ms[kk] for kk in step_kernels)
+    log(f"  sum of the step's kernels {kern_sum * 1e3:.2f} us against the step's {ms_step * 1e3:.2f} us")
+
+    # Cold caches: every rep after a cache-evicting write.  The backward alone
+    # reads the outputs the last forward saved (O, L), as in training.
     cold = timer.cold(step, cold_reps)
     cold_med = statistics.median(cold)
     log(f"  cold step (after a {FLUSH_MIB} MiB write): median {cold_med * 1e3:.2f} us of {cold_reps}")
+    cold_fwd = statistics.median(timer.cold(fwd, cold_reps))
+    step()
+    cold_bwd = statistics.median(timer.cold(bwd, cold_reps))
+    cold_kern = {kname: statistics.median(timer.cold(calls[kname], cold_reps)) for kname in timed_kernels}
+    log(f"  cold fwd {cold_fwd * 1e3:.2f} us, cold bwd {cold_bwd * 1e3:.2f} us, per kernel "
+        + ", ".join(f"{kk} {t * 1e3:.2f}" for kk, t in cold_kern.items()))
 
     ms_graph = None
     if graph:
@@ -354,17 +392,6 @@ def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold
             log(f"  op-level graph step: capture failed ({e})")
     del oq, ok_, ov
 
-    # Per-kernel averages, each kernel in a loop of its own (events between
-    # single launches add their own cost to every launch).  With a one-launch
-    # backward its two stages are timed too, for reference.
-    bwd_launches = _lib.bwd_kernels(a)
-    step_kernels = ("fwd", "bwd") if bwd_launches == 1 else ("fwd", "bwd_dq", "bwd_dkdv")
-    calls = {"fwd": fwd, "bwd": bwd, "bwd_dq": stage(1), "bwd_dkdv": stage(2)}
-    timed_kernels = step_kernels + (("bwd_dq", "bwd_dkdv") if bwd_launches == 1 else ())
-    kern_ms = {kname: timer.loop(calls[kname], steps) for kname in timed_kernels}
-    for kname, t in kern_ms.items():
-        log(f"  {kname}: {t * 1e3:.2f} us/launch" + ("" if kname in step_kernels else " (stage alone)"))
-
     P = w.visible_pairs() * w.B * w.H
     per_pair = {"fwd": 4.0, "bwd_dq": 2.0, "bwd_dkdv": 8.0, "bwd": 10.0}  # algorithmic flop/pair/D per kernel
     total = w.flops_fwd_bwd()
@@ -378,6 +405,9 @@ def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold
         "cold": {
             "step_us_median": round(cold_med * 1e3, 3),
             "tflops": round(total / (cold_med * 1e-3) / 1e12, 3),
+            "fwd_us_median": round(cold_fwd * 1e3, 3),
+            "bwd_us_median": round(cold_bwd * 1e3, 3),
+            "kernel_us_median": {kk: round(t * 1e3, 3) for kk, t in cold_kern.items()},
             "reps": cold_reps,
             "flush": f"{FLUSH_MIB} MiB write before each rep, outside the events",
         },
@@ -385,6 +415,7 @@ def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold
         "op_step_us": round(ms_op * 1e3, 3),
         "op_graph_step_us": round(ms_op_graph * 1e3, 3) if ms_op_graph is not None else None,
         "kernel_us": {kk: round(t * 1e3, 3) for kk, t in kern_ms.items()},
+        "kernel_sum_us": round(kern_sum * 1e3, 3),
         "step_kernels": list(step_kernels),
         "roofline": roofline(w, dom, per_pair[dom] * w.D * P, kern_ms[dom] * 1e-3, peak),
         "config": {
@@ -719,6 +750,7 @@ def main() -> int:
         "op_step_us": head["op_step_us"],
         "op_graph_step_us": head["op_graph_step_us"],
         "kernel_us": head["kernel_us"],
+        "kernel_sum_us": head["kernel_sum_us"],
         "step_kernels": head["step_kernels"],
         "roofline": head["roofline"],
         "peak_fwd_activation_mb": peak_mb,
@@ -731,9 +763,9 @@ def main() -> int:
         for name in ("c3_long_bf16", "c4_nonsoftmax_bf16"):
             if name == w.name:
                 continue
-            r, _ = measure_workload(wl.CONFIGS[name], dev, timer, 20, 5, 0.2, 5, graph=False)
-            if not args.no_native and name == "c3_long_bf16":
-                r["native_harness"] = native_harness(name, 20, 5, 5, 0.2)
+            r, _ = measure_workload(wl.CONFIGS[name], dev, timer, 20, 5, 0.2, 20, graph=False)
+            if not args.no_native:
+                r["native_harness"] = native_harness(name, 20, 5, 20, 0.2)
             result[name.split("_")[0]] = r
             torch.cuda.empty_cache()
     if not args.no_ref_sweep:

@@ -24,7 +24,10 @@
  *    workspaces are owned by the caller.
  *  - All kernels are enqueued on the caller's stream (hipStream_t passed as
  *    void*; NULL = legacy default stream).  Calls never synchronise.
- *  - Calls are re-entrant; the last error message is thread-local.
+ *  - Calls are re-entrant (they keep no state between calls), except
+ *    rbf_attn_bwd_noalloc, whose calls share one workspace per GPU: two of
+ *    them overlapping on one GPU race (see its comment).  The last error
+ *    message is thread-local.
  *  - Return value 0 = success, negative = error code below.
  */
 #ifndef RBF_ATTN_H_
@@ -52,7 +55,7 @@ extern "C" {
 #define RBF_ATTN_EINVAL_ARGS -1    /* null args, bad abi version, bad enum  */
 #define RBF_ATTN_EINVAL_DTYPE -2   /* unknown dtype                         */
 #define RBF_ATTN_EINVAL_STRIDE -3  /* misaligned pointer or stride          */
-#define RBF_ATTN_EINVAL_HEADDIM -4 /* D outside [8, 128] or D % 8 != 0      */
+#define RBF_ATTN_EINVAL_HEADDIM -4 /* D outside [8, 256] or D % 8 != 0      */
 #define RBF_ATTN_EINVAL_SHAPE -5   /* negative sizes, grid too large        */
 #define RBF_ATTN_EINVAL_PTR -6     /* a required pointer is NULL            */
 #define RBF_ATTN_ELAUNCH -7        /* the HIP runtime rejected a launch     */
@@ -137,7 +140,9 @@ int rbf_attn_bwd_stage(const rbf_attn_args* args, void* stream, int stage);
  * RBF_ATTN_NOALLOC_MAX_ROWS (4 MiB of fp32 per GPU); larger problems return
  * RBF_ATTN_EINVAL_SHAPE before any launch.  Every call on a GPU shares that
  * GPU's array: calls that overlap on one GPU (e.g. on two streams) race.
- * The array needs no clearing: each call writes every entry it reads.
+ * The array needs no clearing: each call writes every entry it reads.  The
+ * first call on a device looks the array's address up (in relaxed stream-
+ * capture mode on the calling thread), so that call may itself be captured.
  */
 #define RBF_ATTN_NOALLOC_MAX_ROWS (1 << 20)
 int rbf_attn_bwd_noalloc(const rbf_attn_args* args, void* stream);
@@ -200,7 +205,7 @@ typedef struct rbf_attn_decode_args {
   int32_t dtype;       /* element type of q, k, v, o                         */
   int32_t B, H;
   int32_t T;           /* new query tokens per (b, h): 1 <= T <= 32          */
-  int32_t D;           /* 8 <= D <= 128, D % 8 == 0                          */
+  int32_t D;           /* 8 <= D <= 256, D % 8 == 0                          */
   int32_t L;           /* cache length (maximum over the batch), L >= T      */
   float gamma;         /* RBF bandwidth                                      */
   rbf_attn_tensor q;   /* (B, H, T, D)                                        */

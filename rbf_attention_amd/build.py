@@ -27,16 +27,13 @@ BENCH_NAME = "rbf_attn_bench"
 BENCH_PATH = os.path.join(PKG_DIR, BENCH_NAME)
 ARCH = os.environ.get("RBF_ATTN_ARCH", "gfx950")
 
-# Packed-FP32 VALU ops are disabled for all device code.  MFMA accumulators
-# are kept in ordinary VGPRs (the VGPR form of the MFMA instructions), so the
-# softmax VALU work reads them without AGPR<->VGPR copies.
+# Packed-FP32 VALU ops are disabled for all device code.
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     # NaN never reaches a max/compare on a path whose result is used (masked
     # logits are -inf, never NaN), so fmaxf needs no NaN canonicalisation.
     "-fno-honor-nans",
@@ -54,6 +51,12 @@ COMMON_FLAGS = [
 # 487 us per step).
 HR_FLAGS = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
 STREAM_FLAGS = ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
+# MFMA accumulators are kept in ordinary VGPRs (the VGPR form of the MFMA
+# instructions), so the softmax VALU work reads them without AGPR<->VGPR
+# copies.  Every unit but the fp32 one with 256 features (RBF_WIDE), whose
+# fragments and accumulators exceed 512 registers per lane and on which the
+# compiler fails with this form forced.
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 
 
 def _hipcc() -> str:
@@ -74,12 +77,13 @@ def build(verbose: bool = True) -> str:
     """Compile every HIP translation unit for gfx950 and link librbfattn.so."""
     hipcc = _hipcc()
     units = [
-        ("rbf_attn_capi.hip", []),
-        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=0", *STREAM_FLAGS]),
-        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=1", *STREAM_FLAGS]),
-        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=2", *STREAM_FLAGS]),
-        ("rbf_attn_launch_hr.hip", ["-DRBF_ELEM_ID=0", *HR_FLAGS]),
-        ("rbf_attn_launch_hr.hip", ["-DRBF_ELEM_ID=1", *HR_FLAGS]),
+        ("rbf_attn_capi.hip", VGPR_FORM),
+        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=0", *STREAM_FLAGS, *VGPR_FORM]),
+        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=1", *STREAM_FLAGS, *VGPR_FORM]),
+        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=2", *STREAM_FLAGS, *VGPR_FORM]),
+        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=2", "-DRBF_WIDE", *STREAM_FLAGS]),
+        ("rbf_attn_launch_hr.hip", ["-DRBF_ELEM_ID=0", *HR_FLAGS, *VGPR_FORM]),
+        ("rbf_attn_launch_hr.hip", ["-DRBF_ELEM_ID=1", *HR_FLAGS, *VGPR_FORM]),
     ]
     with tempfile.TemporaryDirectory(prefix="rbfattn_build_") as tmp:
         jobs = []

@@ -5,9 +5,13 @@
 // step (rbf_attn_fwd then rbf_attn_bwd) on its own stream with HIP events:
 //   * warm: after a clock ramp and warm-up steps, K back-to-back steps
 //     between two events;
+//   * per kernel, right after the step loop: fwd, bwd and the backward's two
+//     stages (rbf_attn_bwd_stage 1 and 2) each in a loop of its own of at
+//     least 200 launches and 0.2 s;
 //   * cold: the median over reps of one step timed alone after a 512 MiB
-//     write that evicts L2 and MALL (outside the events);
-//   * fwd and bwd each in a loop of their own.
+//     write that evicts L2 and MALL (outside the events), and likewise of the
+//     forward alone and of the backward alone (from the saved forward
+//     outputs).
 // Prints one JSON line.  Built by rbf_attention_amd/build.py next to
 // librbfattn.so (found through the binary's rpath).
 //
@@ -216,6 +220,8 @@ int main(int argc, char** argv) {
   hip_check(hipEventCreate(&e1), "hipEventCreate");
   auto fwd = [&]() { abi_check(rbf_attn_fwd(&a, st), "rbf_attn_fwd"); };
   auto bwd = [&]() { abi_check(rbf_attn_bwd(&a, st), "rbf_attn_bwd"); };
+  auto dq = [&]() { abi_check(rbf_attn_bwd_stage(&a, st, 1), "rbf_attn_bwd_stage 1"); };
+  auto dkdv = [&]() { abi_check(rbf_attn_bwd_stage(&a, st, 2), "rbf_attn_bwd_stage 2"); };
   auto step = [&]() {
     fwd();
     bwd();
@@ -243,20 +249,37 @@ int main(int argc, char** argv) {
   for (int i = 0; i < warmup; ++i) step();
   const double ms_step = loop(step, steps);
 
-  std::vector<double> cold;
-  for (int r = 0; r < cold_reps; ++r) {
-    hip_check(hipMemsetAsync(flush, r & 0xff, kFlushBytes, st), "hipMemsetAsync");
-    cold.push_back(loop(step, 1));
-  }
-  const double ms_fwd = loop(fwd, steps), ms_bwd = loop(bwd, steps);
+  // one kernel: at least 200 launches and 0.2 s, the count from a short loop
+  auto kernel_loop = [&](auto&& fn) {
+    const double est = loop(fn, 20);
+    long long n = (long long)std::ceil(200.0 / std::max(est, 1e-4));
+    n = std::min<long long>(std::max<long long>(n, 200), 20000);
+    return loop(fn, (int)n);
+  };
+  const double ms_fwd = kernel_loop(fwd), ms_bwd = kernel_loop(bwd);
+  const double ms_dq = kernel_loop(dq), ms_dkdv = kernel_loop(dkdv);
+  const int bwd_launches = rbf_attn_bwd_kernels(&a, nullptr);
+
+  auto cold_median = [&](auto&& fn) {
+    std::vector<double> t;
+    for (int r = 0; r < cold_reps; ++r) {
+      hip_check(hipMemsetAsync(flush, r & 0xff, kFlushBytes, st), "hipMemsetAsync");
+      t.push_back(loop(fn, 1));
+    }
+    return median(t);
+  };
+  const double cold_step = cold_median(step), cold_fwd = cold_median(fwd);
+  step();  // the backward alone reads the outputs the last forward saved
+  const double cold_bwd = cold_median(bwd);
 
   const double P = (double)N * (N + 1) / 2.0 * w.B * w.H;
   const double flops = 14.0 * w.D * P;
   printf("{\"harness\": \"rbf_attn_bench (C ABI, no Python)\", \"workload\": \"%s\", \"steps\": %d, \"warmup\": %d, "
          "\"ramp_steps\": %d, \"step_us\": %.3f, \"tflops\": %.3f, \"fwd_us\": %.3f, \"bwd_us\": %.3f, "
-         "\"cold\": {\"step_us_median\": %.3f, \"reps\": %d}}\n",
+         "\"bwd_dq_us\": %.3f, \"bwd_dkdv_us\": %.3f, \"bwd_launches\": %d, "
+         "\"cold\": {\"step_us_median\": %.3f, \"fwd_us_median\": %.3f, \"bwd_us_median\": %.3f, \"reps\": %d}}\n",
          w.name, steps, warmup, ramp_n, ms_step * 1e3, flops / (ms_step * 1e-3) / 1e12, ms_fwd * 1e3, ms_bwd * 1e3,
-         median(cold) * 1e3, cold_reps);
+         ms_dq * 1e3, ms_dkdv * 1e3, bwd_launches, cold_step * 1e3, cold_fwd * 1e3, cold_bwd * 1e3, cold_reps);
 
   hip_check(hipStreamSynchronize(st), "sync");
   hip_check(hipEventDestroy(e0), "hipEventDestroy");

@@ -53,8 +53,8 @@ int check_common(const rbf_attn_args* a) {
     return fail(RBF_ATTN_EINVAL_DTYPE, "unknown dtype %d", a->dtype);
   if (a->B < 0 || a->H < 0 || a->N < 0)
     return fail(RBF_ATTN_EINVAL_SHAPE, "negative size B=%d H=%d N=%d", a->B, a->H, a->N);
-  if (a->D < 8 || a->D > 128 || a->D % 8 != 0)
-    return fail(RBF_ATTN_EINVAL_HEADDIM, "head dim D=%d unsupported (need 8 <= D <= 128, D %% 8 == 0)", a->D);
+  if (a->D < 8 || a->D > 256 || a->D % 8 != 0)
+    return fail(RBF_ATTN_EINVAL_HEADDIM, "head dim D=%d unsupported (need 8 <= D <= 256, D %% 8 == 0)", a->D);
   if (a->causal != 0 && a->causal != 1) return fail(RBF_ATTN_EINVAL_ARGS, "causal must be 0 or 1");
   if (a->num_prefix < 0) return fail(RBF_ATTN_EINVAL_ARGS, "num_prefix must be >= 0");
   if (!(a->gamma > 0.f) || !isfinite(a->gamma))
@@ -153,22 +153,24 @@ int decode_check(const rbf_attn_decode_args* a, DecodeGeom* g) {
   if (a->B < 0 || a->H < 0) return fail(RBF_ATTN_EINVAL_SHAPE, "negative size B=%d H=%d", a->B, a->H);
   if (a->T < 1 || a->T > 32) return fail(RBF_ATTN_EINVAL_SHAPE, "T=%d query tokens unsupported (need 1..32)", a->T);
   if (a->L < a->T || a->L > (1 << 30)) return fail(RBF_ATTN_EINVAL_SHAPE, "cache length L=%d must be in [T, 2^30]", a->L);
-  if (a->D < 8 || a->D > 128 || a->D % 8 != 0)
-    return fail(RBF_ATTN_EINVAL_HEADDIM, "head dim D=%d unsupported (need 8 <= D <= 128, D %% 8 == 0)", a->D);
+  if (a->D < 8 || a->D > 256 || a->D % 8 != 0)
+    return fail(RBF_ATTN_EINVAL_HEADDIM, "head dim D=%d unsupported (need 8 <= D <= 256, D %% 8 == 0)", a->D);
   if (!(a->gamma > 0.f) || !isfinite(a->gamma))
     return fail(RBF_ATTN_EINVAL_ARGS, "gamma must be finite and > 0 (got %g)", (double)a->gamma);
   const long long bh = (long long)a->B * a->H;
   if (bh > 0x7fffffffLL / 32) return fail(RBF_ATTN_EINVAL_SHAPE, "B*H=%lld too large", bh);
-  g->dp = a->D <= 32 ? 32 : a->D <= 64 ? 64 : 128;
+  g->dp = a->D <= 32 ? 32 : a->D <= 64 ? 64 : a->D <= 128 ? 128 : 256;
   // Split the key axis into one round of work-groups: as many as fit on the
   // 256 CUs at once (2 per CU for 128 features, whose split kernel holds 256
-  // VGPRs and 68 KB of LDS; 3 otherwise).  One round measured 7-20 % faster
-  // than two or more (no tail).  RBF_ATTN_DECODE_WGS overrides (sweeps).
+  // VGPRs and 68 KB of LDS; 1 for 256 features, whose V tiles take 135 KB;
+  // 3 otherwise).  One round measured 7-20 % faster than two or more (no
+  // tail).  RBF_ATTN_DECODE_WGS overrides (sweeps).
   g->waves = rbf::decode_waves(a->dtype == RBF_ATTN_FP32);
   const int tile = 32 * g->waves;
   const int ntiles = (a->L + tile - 1) / tile;
   static const long long forced = getenv("RBF_ATTN_DECODE_WGS") ? atoll(getenv("RBF_ATTN_DECODE_WGS")) : 0;
-  const long long target = forced > 0 ? forced : (g->dp == 128 || a->dtype == RBF_ATTN_FP32 ? 512 : 768);
+  const long long target =
+      forced > 0 ? forced : (g->dp == 256 ? 256 : g->dp == 128 || a->dtype == RBF_ATTN_FP32 ? 512 : 768);
   long long ns = bh > 0 ? (target + bh - 1) / bh : 1;
   if (ns > ntiles) ns = ntiles;
   if (ns < 1) ns = 1;
@@ -205,11 +207,20 @@ int scratch_ptr(hipStream_t stream, float** out) {
   if (dev < 0 || dev >= kMaxDevices) return fail(RBF_ATTN_ELAUNCH, "device %d out of range", dev);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
-    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess)
+    // The first call on a device may come while the caller's stream is being
+    // captured into a graph: the lookup (and any device switch) then runs in
+    // relaxed capture mode on this thread, which admits calls that global or
+    // thread-local capture would reject, and the caller's mode is restored.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const bool swapped = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) {
+      if (swapped) (void)hipThreadExchangeStreamCaptureMode(&mode);
       return fail(RBF_ATTN_ELAUNCH, "hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+    }
     void* ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (dev != cur) (void)hipSetDevice(cur);
+    if (swapped) (void)hipThreadExchangeStreamCaptureMode(&mode);
     if (e != hipSuccess || ptr == nullptr)
       return fail(RBF_ATTN_ELAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
     g_scratch_ptr[dev] = static_cast<float*>(ptr);

@@ -249,15 +249,23 @@ __device__ inline float xhalf_max(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// Sum over aligned groups of G consecutive lanes (G in {1, 2, 4, 8, 16}) with
-// DPP lane moves; every lane of a group receives the group sum.
+// Sum over lanes l and l ^ 16 (v_permlane16_swap).
+__device__ inline float xrow_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum over aligned groups of G consecutive lanes (G in {1, 2, 4, 8, 16, 32})
+// with DPP lane moves (and one permlane16 swap for 32); every lane of a group
+// receives the group sum.
 template <int G>
 __device__ inline float group_sum(float x) {
   if constexpr (G >= 2) x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
   if constexpr (G >= 4) x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
   if constexpr (G >= 8) x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));
   if constexpr (G >= 16) x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));
-  static_assert(G <= 16, "group_sum supports groups of at most 16 lanes");
+  if constexpr (G >= 32) x = xrow_sum(x);
+  static_assert(G <= 32, "group_sum supports groups of at most 32 lanes");
   return x;
 }
 
@@ -454,12 +462,6 @@ __device__ inline typename Elem<T>::frag ld_trc(const T* tile, int tbase, int fb
   typedef short s16x8_t __attribute__((ext_vector_type(8)));
   const s16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   return __builtin_bit_cast(typename Elem<T>::frag, v);
-}
-
-// Sum over lanes l and l ^ 16 (v_permlane16_swap).
-__device__ inline float xrow_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Cooperative chunk-major tile, staged global -> registers -> LDS.  Work
@@ -1133,10 +1135,13 @@ __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int gr
   typedef TileLayout<T, BN, DP, DMA || kChunkMajor<T, DP>> TLy;
   static_assert(!DMA || TR, "LDS-DMA staging is for 16-bit tiles");
   constexpr int TSZ = TLy::SIZE;
-  // register staging: two buffers each (a single element when DMA)
-  constexpr int NB2 = DMA ? 1 : 2;
+  // register staging: two buffers each (a single element when DMA).  fp32
+  // tiles of 256 features (K, K^T, V: 104 KB per buffer) fit LDS only once:
+  // SB single-buffers them, with a barrier before each tile's stores.
+  constexpr bool SB = !TR && DP > 128;
+  constexpr int NB2 = (DMA || SB) ? 1 : 2;
   __shared__ __attribute__((aligned(16))) T sK[NB2][DMA ? 8 : TSZ];
-  __shared__ __attribute__((aligned(16))) T sKt[TR ? 1 : 2][TR ? 8 : DP * LDT];
+  __shared__ __attribute__((aligned(16))) T sKt[TR ? 1 : NB2][TR ? 8 : DP * LDT];
   __shared__ __attribute__((aligned(16))) T sV[NB2][DMA ? 8 : TSZ];
   auto roff = [](int row, int col) { return TLy::off(row, col); };
   __shared__ __attribute__((aligned(16))) float sKn[NB2][DMA ? 1 : BN];
@@ -1308,7 +1313,8 @@ __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int gr
     tk.load(K, p.sk[2], tok0_of(0), N, D, tid);
     tv.load(V, p.sv[2], tok0_of(0), N, D, tid);
     for (int kt = 0; kt < nkt; ++kt) {
-      const int buf = kt & 1;
+      const int buf = SB ? 0 : (kt & 1);
+      if (SB && kt > 0) __syncthreads();  // every wave is done with tile kt - 1
       if constexpr (TR) {
         TLy::store(tk, sK[buf], tid);
         TLy::store(tv, sV[buf], tid);
@@ -1391,13 +1397,16 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
   static_assert(!DMA || (TR && BM % 64 == 0), "LDS-DMA staging: 16-bit tiles of whole 64-row groups");
   constexpr int TSZ = TLy::SIZE;
   // register staging: two buffers each; LDS-DMA staging: three (the other
-  // form's arrays shrink to a single element)
-  constexpr int NB2 = DMA ? 1 : 2, NB3 = DMA ? 3 : 1;
+  // form's arrays shrink to a single element).  fp32 tiles of 256 features
+  // (Q, Q^T, dO, dO^T: 140 KB per buffer) fit LDS only once: SB
+  // single-buffers them, with a barrier before each tile's stores.
+  constexpr bool SB = !TR && DP > 128;
+  constexpr int NB2 = (DMA || SB) ? 1 : 2, NB3 = DMA ? 3 : 1;
   __shared__ __attribute__((aligned(16))) T sQ[NB2][DMA ? 8 : TSZ];
-  __shared__ __attribute__((aligned(16))) T sQt[TR ? 1 : 2][TR ? 8 : DP * LDT];
+  __shared__ __attribute__((aligned(16))) T sQt[TR ? 1 : NB2][TR ? 8 : DP * LDT];
   __shared__ __attribute__((aligned(16))) T sD[NB2][DMA ? 8 : TSZ];
   auto roff = [](int row, int col) { return TLy::off(row, col); };
-  __shared__ __attribute__((aligned(16))) T sDt[TR ? 1 : 2][TR ? 8 : DP * LDT];
+  __shared__ __attribute__((aligned(16))) T sDt[TR ? 1 : NB2][TR ? 8 : DP * LDT];
   __shared__ __attribute__((aligned(16))) float sOff[NB2][DMA ? 1 : BM];
   __shared__ __attribute__((aligned(16))) float sDel[NB2][DMA ? 1 : BM];
   __shared__ __attribute__((aligned(16))) T dQt[NB3][DMA ? TSZ : 8];
@@ -1668,7 +1677,8 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
   } else {
     load_tile(qt_lo);
     for (int qt = qt_lo; qt < nqt_all; ++qt) {
-      const int buf = qt & 1;
+      const int buf = SB ? 0 : (qt & 1);
+      if (SB && qt > qt_lo) __syncthreads();  // every wave is done with tile qt - 1
       if constexpr (TR) {
         TLy::store(tq, sQ[buf], tid);
         TLy::store(td, sD[buf], tid);

@@ -26,6 +26,13 @@ RBF_DECLARE_LAUNCHERS(fp32)
 
 #undef RBF_DECLARE_LAUNCHERS
 
+// fp32 kernels with 256 features, compiled in a unit of their own
+// (rbf_attn_launch.hip with RBF_WIDE, register classes left to the compiler).
+hipError_t launch_fwd_wide_fp32(const Params& p, int variant, hipStream_t st);
+hipError_t launch_bwd_dq_wide_fp32(const Params& p, int variant, hipStream_t st);
+hipError_t launch_bwd_dkdv_wide_fp32(const Params& p, int variant, hipStream_t st);
+hipError_t launch_decode_wide_fp32(const DecodeParams& p, int variant, hipStream_t st);
+
 // Head-resident kernels (16-bit elements, 32 < D <= 64, N <= 32 * kHrMaxBlocks;
 // defined in rbf_attn_launch_hr.hip).  They return hipErrorInvalidValue for
 // shapes they do not cover.

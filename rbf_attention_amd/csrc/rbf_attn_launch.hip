@@ -1,6 +1,7 @@
 // Launchers for one element type.  Compiled once per dtype with
 // -DRBF_ELEM_ID=0 (bf16), 1 (fp16) or 2 (fp32), so the three instantiation
-// sets build in parallel.
+// sets build in parallel; once more with -DRBF_ELEM_ID=2 -DRBF_WIDE for the
+// fp32 kernels with 256 features (launch_*_wide_fp32).
 //
 // A kernel configuration is (W waves per work-group, blocks of 32 tokens per
 // wave, LDS tile of streamed tokens).  Defaults per padded head dim DP are in
@@ -11,10 +12,14 @@
 
 #include "rbf_attn_kernels.h"
 #include "rbf_attn_launch.h"
+#include "rbf_attn_staging.h"
 #include "rbf_decode_kernels.h"
 
 #ifndef RBF_ELEM_ID
 #error "RBF_ELEM_ID must be defined (0 bf16, 1 fp16, 2 fp32)"
+#endif
+#if defined(RBF_WIDE) && RBF_ELEM_ID != 2
+#error "RBF_WIDE builds the fp32 kernels with 256 features only"
 #endif
 
 namespace rbf {
@@ -156,14 +161,15 @@ constexpr int kHrBlocks64 = kHrMaxBlocks;  // D <= 64: N <= 576
 
 // LDS-DMA tile staging (16-bit, D = 64 or 128 filling the padded width DP:
 // the streaming kernels' tiles go from global memory straight into LDS, three
-// tiles in flight).  The DMA reads whole DP-wide rows through buffer
-// resources whose byte range (N rows of each slice) must stay below 2^31.
-// RBF_ATTN_DMA=0 keeps the register-staged kernels.
-bool dma_fits(int64_t N, int64_t stride) { return N * stride * (int64_t)sizeof(Elt) < (int64_t(1) << 31); }
+// tiles in flight), for operands whose rows dma_rows_ok admits
+// (rbf_attn_staging.h); others take the register-staged kernels.
+// RBF_ATTN_DMA=0 keeps the register-staged kernels for every shape.
 bool use_dma(const Params& p, int dp) {
   static const int forced = env_choice("RBF_ATTN_DMA");
-  return !kIsF32 && forced != 0 && p.D == dp && dma_fits(p.N, p.sk[2]) && dma_fits(p.N, p.sv[2]) &&
-         dma_fits(p.N, p.sq[2]) && dma_fits(p.N, p.sdo[2]);
+  constexpr int64_t esz = sizeof(Elt);
+  return !kIsF32 && forced != 0 && p.D == dp && dma_rows_ok(p.N, p.sk[2], p.D, esz) &&
+         dma_rows_ok(p.N, p.sv[2], p.D, esz) && dma_rows_ok(p.N, p.sq[2], p.D, esz) &&
+         dma_rows_ok(p.N, p.sdo[2], p.D, esz);
 }
 
 template <int DP, bool SM, int W, int BN, bool BIN = false, bool DMA = false>
@@ -217,7 +223,12 @@ hipError_t fwd_default(const Params& p, hipStream_t st) {
     if (use_hr(p, kHrBlocks64, 1)) return hr_fwd(p, SM, 12, st);
   }
   if constexpr (kIsF32) return fwd_cfg<DP, SM, 4, 32>(p, st);
-  else if constexpr (DP <= 64) {
+  else if constexpr (DP == 256) {
+    // 256 features: Q^T fragments and O^T accumulators of a 32-query block
+    // take 192 registers, so one wave per SIMD (AGPRs hold the overflow, no
+    // scratch); K and V tiles through registers into padded row-major LDS.
+    return fwd_cfg<DP, SM, 4, 64>(p, st);
+  } else if constexpr (DP <= 64) {
     // LDS-DMA: 4 waves over 64-key tiles at every length, one group per
     // work-group.  The bin loop re-primes the three-tile pipeline for each of
     // its groups with nothing to overlap it; separate work-groups overlap one
@@ -250,8 +261,11 @@ hipError_t dq_default(const Params& p, hipStream_t st) {
   if constexpr (!kIsF32 && DP == 64) {
     if (use_hr(p, kHrBlocks64, 2)) return hr_dq(p, SM, st);
   }
-  if constexpr (kIsF32) return dq_cfg<DP, SM, 4, 1, 32>(p, st);
-  else if constexpr (DP <= 64) {
+  if constexpr (kIsF32) return dq_cfg<DP, SM, 4, 1, 32, DP != 256>(p, st);
+  else if constexpr (DP == 256) {
+    // 32-key tiles, K^T read next to the dQ MFMAs (one wave per SIMD)
+    return dq_cfg<DP, SM, 4, 1, 32, false>(p, st);
+  } else if constexpr (DP <= 64) {
     // (LDS-DMA on 64-key tiles: three 128-key tiles leave room for one
     // four-wave work-group per CU.)  One group per work-group, as for the
     // forward: against the binned form (bf16 softmax dQ, us) B63 H8 N1028 192
@@ -285,8 +299,13 @@ hipError_t dkdv_default(const Params& p, hipStream_t st) {
   if constexpr (!kIsF32 && DP == 64) {
     if (use_hr(p, kHrBlocks64, 4)) return hr_dkdv(p, SM, st);
   }
-  if constexpr (kIsF32) return dkdv_cfg<DP, SM, 4, 1, 32>(p, st);
-  else if constexpr (DP <= 64) {
+  if constexpr (kIsF32) return dkdv_cfg<DP, SM, 4, 1, 32, DP != 256>(p, st);
+  else if constexpr (DP == 256) {
+    // the paired kernel with two key blocks (four waves) per work-group over
+    // 64-query register-staged tiles: each wave holds one of K, V and one
+    // 32 x 256 accumulator
+    return dkdv_pair_cfg<DP, SM, 2, 64>(p, st);
+  } else if constexpr (DP <= 64) {
     // LDS-DMA from N = 4096 on: at N = 512-2048 the D = 64 dK/dV measured as
     // fast or slower with it (C4 188 -> 191 us), at N = 8192 faster (605 -> 589).
     // With it, one group per work-group (as the forward and dQ): 0.7-3.4 %
@@ -432,20 +451,63 @@ hipError_t dkdv_any_cfg(const Params& p, hipStream_t st) {
   return dkdv_default<DP, SM>(p, st);
 }
 
-// Head dim D (a multiple of 8 in [8, 128]) runs on the kernel for the next
-// padded width DP in {32, 64, 128}; features D..DP-1 are zero-filled.  Only
-// the softmax bf16 path with D in (32, 64] carries tuning candidates.
-#define RBF_DISPATCH(DEF, ANY)                                                      \
+template <int DP, bool SM>
+hipError_t decode_dp(const DecodeParams& p, hipStream_t st) {
+  constexpr int W = kIsF32 ? 2 : 4;
+  if (p.W != W) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((rbf_decode_split_kernel<Elt, DP, W, SM>), dim3(p.B * p.H, p.nsplit), dim3(64 * W), 0, st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((rbf_decode_merge_kernel<Elt, DP, SM>), dim3(p.B * p.H * p.T), dim3(64), 0, st, p);
+  return hipGetLastError();
+}
+
+#ifndef RBF_WIDE
+// 256 features.  The fp32 kernels of that width are built in a unit of their
+// own (this file with RBF_WIDE): their register-resident Q/K/V/dO fragments
+// and accumulators exceed the 512 registers of a lane, and with the VGPR form
+// of the MFMA instructions forced (as for every other kernel) the compiler
+// fails on them, so that unit leaves the register classes to the compiler.
+hipError_t fwd_256(const Params& p, bool sm, hipStream_t st) {
+#if RBF_ELEM_ID == 2
+  return launch_fwd_wide_fp32(p, sm ? 0 : 1, st);
+#else
+  return sm ? fwd_default<256, true>(p, st) : fwd_default<256, false>(p, st);
+#endif
+}
+hipError_t dq_256(const Params& p, bool sm, hipStream_t st) {
+#if RBF_ELEM_ID == 2
+  return launch_bwd_dq_wide_fp32(p, sm ? 0 : 1, st);
+#else
+  return sm ? dq_default<256, true>(p, st) : dq_default<256, false>(p, st);
+#endif
+}
+hipError_t dkdv_256(const Params& p, bool sm, hipStream_t st) {
+#if RBF_ELEM_ID == 2
+  return launch_bwd_dkdv_wide_fp32(p, sm ? 0 : 1, st);
+#else
+  return sm ? dkdv_default<256, true>(p, st) : dkdv_default<256, false>(p, st);
+#endif
+}
+
+// Head dim D (a multiple of 8 in [8, 256]) runs on the kernel for the next
+// padded width DP in {32, 64, 128, 256}; features D..DP-1 are zero-filled (as
+// the reference pads to BLOCK_DMODEL = next_pow2(D), rbf_attention.py:661).
+// Only the softmax bf16 path with D in (32, 128] carries tuning candidates.
+#define RBF_DISPATCH(DEF, ANY, W256)                                                \
   do {                                                                              \
     const bool sm = (variant == 0);                                                 \
     if (p.D <= 32) return sm ? DEF<32, true>(p, st) : DEF<32, false>(p, st);        \
     if (p.D <= 64) return sm ? ANY<64, true>(p, st) : DEF<64, false>(p, st);        \
-    return sm ? ANY<128, true>(p, st) : DEF<128, false>(p, st);                     \
+    if (p.D <= 128) return sm ? ANY<128, true>(p, st) : DEF<128, false>(p, st);     \
+    return W256(p, sm, st);                                                         \
   } while (0)
 
-hipError_t fwd_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(fwd_default, fwd_any_cfg); }
-hipError_t dq_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(dq_default, dq_any_cfg); }
-hipError_t dkdv_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(dkdv_default, dkdv_any_cfg); }
+hipError_t fwd_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(fwd_default, fwd_any_cfg, fwd_256); }
+hipError_t dq_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(dq_default, dq_any_cfg, dq_256); }
+hipError_t dkdv_any(const Params& p, int variant, hipStream_t st) {
+  RBF_DISPATCH(dkdv_default, dkdv_any_cfg, dkdv_256);
+}
 
 #undef RBF_DISPATCH
 
@@ -471,26 +533,36 @@ hipError_t bwd_any(const Params& p, int variant, hipStream_t st) {
   return dkdv_any(p, variant, st);
 }
 
-template <int DP, bool SM>
-hipError_t decode_dp(const DecodeParams& p, hipStream_t st) {
-  constexpr int W = kIsF32 ? 2 : 4;
-  if (p.W != W) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((rbf_decode_split_kernel<Elt, DP, W, SM>), dim3(p.B * p.H, p.nsplit), dim3(64 * W), 0, st, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((rbf_decode_merge_kernel<Elt, DP, SM>), dim3(p.B * p.H * p.T), dim3(64), 0, st, p);
-  return hipGetLastError();
-}
-
 hipError_t decode_any(const DecodeParams& p, int variant, hipStream_t st) {
   const bool sm = variant == 0;
   if (p.D <= 32) return sm ? decode_dp<32, true>(p, st) : decode_dp<32, false>(p, st);
   if (p.D <= 64) return sm ? decode_dp<64, true>(p, st) : decode_dp<64, false>(p, st);
-  return sm ? decode_dp<128, true>(p, st) : decode_dp<128, false>(p, st);
+  if (p.D <= 128) return sm ? decode_dp<128, true>(p, st) : decode_dp<128, false>(p, st);
+#if RBF_ELEM_ID == 2
+  return launch_decode_wide_fp32(p, variant, st);
+#else
+  return sm ? decode_dp<256, true>(p, st) : decode_dp<256, false>(p, st);
+#endif
 }
+#endif  // !RBF_WIDE
 
 }  // namespace
 
+#ifdef RBF_WIDE
+// fp32 kernels with 256 features (see fwd_256).
+hipError_t launch_fwd_wide_fp32(const Params& p, int variant, hipStream_t st) {
+  return variant == 0 ? fwd_default<256, true>(p, st) : fwd_default<256, false>(p, st);
+}
+hipError_t launch_bwd_dq_wide_fp32(const Params& p, int variant, hipStream_t st) {
+  return variant == 0 ? dq_default<256, true>(p, st) : dq_default<256, false>(p, st);
+}
+hipError_t launch_bwd_dkdv_wide_fp32(const Params& p, int variant, hipStream_t st) {
+  return variant == 0 ? dkdv_default<256, true>(p, st) : dkdv_default<256, false>(p, st);
+}
+hipError_t launch_decode_wide_fp32(const DecodeParams& p, int variant, hipStream_t st) {
+  return variant == 0 ? decode_dp<256, true>(p, st) : decode_dp<256, false>(p, st);
+}
+#else
 #if RBF_ELEM_ID == 0
 #define RBF_NAME bf16
 #elif RBF_ELEM_ID == 1
@@ -517,5 +589,6 @@ int RBF_CAT(bwd_kernels_, RBF_NAME)(const Params& p) { return bwd_one_launch(p) 
 hipError_t RBF_CAT(launch_decode_, RBF_NAME)(const DecodeParams& p, int variant, hipStream_t st) {
   return decode_any(p, variant, st);
 }
+#endif  // RBF_WIDE
 
 }  // namespace rbf

@@ -54,8 +54,8 @@ def _check_inputs(name: str, *ts: torch.Tensor) -> None:
             raise ValueError(f"{name}: device mismatch {t.device} vs {q.device}")
     if q.dtype not in _lib.DTYPE_CODES:
         raise TypeError(f"{name}: unsupported dtype {q.dtype} (bf16, fp16, fp32)")
-    if q.shape[-1] > 128:
-        raise ValueError(f"{name}: head dim {q.shape[-1]} > 128 is not supported")
+    if q.shape[-1] > 256:
+        raise ValueError(f"{name}: head dim {q.shape[-1]} > 256 is not supported")
     if q.device.type != "cuda":
         raise RuntimeError(
             f"{name}: tensors are on {q.device}; the RBF attention kernels run only on a ROCm GPU "
@@ -495,8 +495,8 @@ def _decode(q, k_cache, v_cache, cache_lens, softmax: bool, sm_scale: float):
         raise TypeError(f"decode: unsupported dtype {q.dtype} (bf16, fp16, fp32)")
     if q.device.type != "cuda":
         raise RuntimeError("decode: the kernels run only on a ROCm GPU (there is no CPU fallback)")
-    if D > 128:
-        raise ValueError(f"decode: head dim {D} > 128 is not supported")
+    if D > 256:
+        raise ValueError(f"decode: head dim {D} > 256 is not supported")
     if not 1 <= T <= 32:
         raise ValueError(f"decode: {T} query tokens per step unsupported (1..32)")
     L = k_cache.shape[2]

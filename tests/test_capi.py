@@ -86,7 +86,8 @@ def call(lib, fn, a):
         (dict(variant=5), -1),
         (dict(dtype=7), -2),
         (dict(D=60), -4),
-        (dict(D=136), -4),
+        (dict(D=132), -4),
+        (dict(D=264), -4),
         (dict(D=0), -4),
         (dict(B=-1), -5),
         (dict(causal=2), -1),
@@ -262,9 +263,12 @@ def test_decode_workspace_size(lib):
     # 128 (b, h) pairs, 16K keys, 128 features: 512 work-groups = 4 splits
     big = decode_args(B=8, H=16, T=1, D=128, L=16384)
     assert lib.rbf_attn_decode_workspace_size(ctypes.byref(big)) == 128 * 16 * 1 * 130 * 4
+    # 256 features: one work-group per CU, 256 in total = 2 splits x 4 waves
+    wide = decode_args(B=8, H=16, T=1, D=256, L=16384)
+    assert lib.rbf_attn_decode_workspace_size(ctypes.byref(wide)) == 128 * 8 * 1 * 258 * 4
 
 
-@pytest.mark.parametrize("over", [dict(T=0), dict(T=33), dict(L=0), dict(T=4, L=3), dict(D=12), dict(D=136),
+@pytest.mark.parametrize("over", [dict(T=0), dict(T=33), dict(L=0), dict(T=4, L=3), dict(D=12), dict(D=264),
                                   dict(gamma=0.0), dict(variant=2), dict(dtype=5), dict(abi_version=0)])
 def test_decode_validation(lib, over):
     a = decode_args(**over)

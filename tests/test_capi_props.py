@@ -42,7 +42,7 @@ def base_args(B, H, N, D, dtype, variant, causal, num_prefix, gamma):
 
 valid = st.fixed_dictionaries(dict(
     B=st.integers(1, 64), H=st.integers(1, 64), N=st.integers(1, 20000),
-    D=st.sampled_from(range(8, 129, 8)), dtype=st.sampled_from((0, 1, 2)), variant=st.sampled_from((0, 1)),
+    D=st.sampled_from(range(8, 257, 8)), dtype=st.sampled_from((0, 1, 2)), variant=st.sampled_from((0, 1)),
     causal=st.sampled_from((0, 1)), num_prefix=st.integers(0, 600),
     gamma=st.floats(1e-4, 10.0, allow_nan=False, allow_infinity=False)))
 
@@ -63,7 +63,7 @@ def _bad_dtype(a, d):
 
 
 def _bad_headdim(a, d):
-    a.D = d(st.sampled_from((0, 4, 12, 60, 100, 136, 256, -8)))
+    a.D = d(st.sampled_from((0, 4, 12, 60, 100, 132, 264, 512, -8)))
     return HEADDIM
 
 

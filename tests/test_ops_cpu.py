@@ -58,7 +58,7 @@ def test_shape_and_dtype_checks():
         ra.run_triton_rbf(q, q.double(), q)
     with pytest.raises(ValueError):
         ra.run_triton_rbf(q[0], q[0], q[0])
-    big = torch.randn(1, 1, 4, 136)
+    big = torch.randn(1, 1, 4, 264)
     with pytest.raises(ValueError):
         ra.run_triton_rbf(big, big, big)
 

@@ -218,35 +218,34 @@ def test_c2_registers_visible_to_all(cuda_device):
     compare_case(q, k, v, do, gamma=w.sm_scale, num_prefix=4, tag="C2-prefix4")
 
 
-_C3 = {}
-
-
-def c3_outputs(dev):
-    """C3 inputs and kernel outputs, computed once for the slice checks."""
-    if not _C3:
-        w = wl.C3_LONG
-        q, k, v, do = to_dev(wl.make_inputs(w), dev)
-        _C3["inputs"] = (q, k, v, do)
-        _C3["outs"] = run_ours(q, k, v, do, True, True, w.sm_scale, 0)
-    return _C3["inputs"], _C3["outs"]
+@pytest.fixture(scope="module")
+def c3_run(cuda_device):
+    """C3 inputs and kernel outputs (about 1 GiB on the GPU), computed once for
+    the slice checks and freed when the module's tests are done, whichever of
+    them run and in whatever order."""
+    w = wl.C3_LONG
+    q, k, v, do = to_dev(wl.make_inputs(w), cuda_device)
+    outs = run_ours(q, k, v, do, True, True, w.sm_scale, 0)
+    yield (q, k, v, do), outs
+    del q, k, v, do, outs
+    torch.cuda.empty_cache()
 
 
 @pytest.mark.parametrize("b,h", [(0, 0), (1, 5), (2, 10), (3, 15)])
-def test_c3_long_bf16_sampled(cuda_device, b, h):
+def test_c3_long_bf16_sampled(c3_run, b, h):
     """Four (b, h) slices of C3 against the oracle, the last head included."""
-    (q, k, v, do), outs = c3_outputs(cuda_device)
+    (q, k, v, do), outs = c3_run
     sl = (slice(b, b + 1), slice(h, h + 1))
     compare_case(q, k, v, do, gamma=wl.C3_LONG.sm_scale, sl=sl, tag=f"C3 b{b}h{h}", outs=outs)
 
 
-def test_c3_long_bf16_full_size_properties(cuda_device):
+def test_c3_long_bf16_full_size_properties(c3_run):
     """Finite everywhere; the zero register row 0 sees only key 0 (v_0 = 0),
     so O[:, :, 0] == 0 exactly."""
-    _, outs = c3_outputs(cuda_device)
+    _, outs = c3_run
     for t in outs:
         assert torch.isfinite(t).all()
     assert (outs[0][:, :, 0] == 0).all()
-    _C3.clear()
 
 
 def test_c4_nonsoftmax_bf16_sampled(cuda_device):
@@ -456,6 +455,42 @@ def test_strided_views_dma_tiles(cuda_device, D, N, dtype, softmax):
     for sl in ((slice(0, 1), slice(0, 1)), (slice(B - 1, B), slice(H - 1, H))):
         compare_case(q, k, v, do, softmax=softmax, gamma=gamma, sl=sl, outs=outs,
                      tag=f"strided D{D} N{N} b{sl[0].start}h{sl[1].start}")
+
+
+@pytest.mark.parametrize(
+    "D,N,which,softmax",
+    [(64, 700, "kv", True), (128, 2113, "kv", True), (128, 2113, "qdo", True), (64, 4200, "qdo", False),
+     (128, 2113, "kv", False)],
+)
+def test_zero_token_stride_operands(cuda_device, D, N, which, softmax):
+    """Operands expanded along the token axis (x.expand(B, H, N, D): token
+    stride 0), passed to the ops as they are.  Such rows cannot be staged by
+    LDS-DMA, whose buffer range is N * stride bytes (empty at stride 0), so
+    the launchers take the register-staged kernels for them; the shapes are
+    ones whose contiguous operands take LDS-DMA tiles (D = 64 at N = 700:
+    forward and dQ; D = 128 at N = 2113: forward, dQ and dK/dV; D = 64 at
+    N = 4200: dK/dV).  "kv": K and V expanded (the tiles of the forward and
+    dQ), "qdo": Q and dO expanded (the tiles of dK/dV)."""
+    B, H = 1, 2
+    q, k, v, do = rand_inputs(B, H, N, D, torch.bfloat16, cuda_device, std=1.0 if softmax else 0.5, seed=N + D)
+    if which == "kv":
+        k = k[:, :, 5:6].expand(B, H, N, D)
+        v = v[:, :, 7:8].expand(B, H, N, D)
+        assert k.stride(2) == 0 and v.stride(2) == 0
+    else:
+        q = q[:, :, 3:4].expand(B, H, N, D)
+        do = do[:, :, 9:10].expand(B, H, N, D)
+        assert q.stride(2) == 0 and do.stride(2) == 0
+    gamma = 1.0 / (2 * math.sqrt(D))
+    if softmax:
+        out, L = torch.ops.rbf_attn_amd.scaled_fwd_ex(q, k, v, True, gamma, 0)
+        grads = torch.ops.rbf_attn_amd.scaled_bwd_ex(q, k, v, out, L, do, True, gamma, 0)
+    else:
+        out = torch.ops.rbf_attn_amd.non_softmax_fwd_ex(q, k, v, True, gamma, 0)
+        grads = torch.ops.rbf_attn_amd.non_softmax_bwd_ex(q, k, v, do, True, gamma, 0)
+    torch.cuda.synchronize()
+    compare_case(q, k, v, do, softmax=softmax, gamma=gamma, outs=(out,) + tuple(grads),
+                 tag=f"stride0 {which} D{D} N{N} sm{softmax}")
 
 
 @pytest.mark.parametrize("softmax", [True, False])

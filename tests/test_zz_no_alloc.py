@@ -2,7 +2,10 @@
 library's static device array) against rbf_attn_bwd (caller workspace),
 through the C ABI: bit-identical dq, dk, dv on two calls in a row, the
 second with a smaller problem, for both variants and both backward forms
-(one head-resident launch, and the two streaming launches)."""
+(one head-resident launch, and the two streaming launches); captured in a
+HIP graph (the first call of the process, so that the per-device lookup of
+the array runs under capture) and replayed; and at the largest problem the
+array holds, B * H * N = RBF_ATTN_NOALLOC_MAX_ROWS."""
 import math
 
 import pytest
@@ -48,6 +51,36 @@ def run_pair(bufs, a, sp):
     return ref, [bufs[f] for f in ("dq", "dk", "dv")]
 
 
+def test_noalloc_graph_capture_replays(cuda_device):
+    """The entry point is for callers under graph capture: captured (as the
+    process's first call of it, when run first in a fresh process or in the
+    suite), its replays reproduce rbf_attn_bwd bit for bit, three times, with
+    the outputs cleared and eager work run between the replays."""
+    bufs, a = make(2, 4, 700, 128, torch.bfloat16, cuda_device, True, seed=31)
+    sp = torch.cuda.current_stream(cuda_device).cuda_stream
+    _lib.call("rbf_attn_fwd", a, sp)
+    _lib.call("rbf_attn_bwd", a, sp)
+    torch.cuda.synchronize()
+    ref = [bufs[f].clone() for f in ("dq", "dk", "dv")]
+    a.delta = None
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(cuda_device)
+    side.wait_stream(torch.cuda.current_stream(cuda_device))
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            _lib.call("rbf_attn_bwd_noalloc", a, torch.cuda.current_stream(cuda_device).cuda_stream)
+    torch.cuda.current_stream(cuda_device).wait_stream(side)
+    for rep in range(3):
+        for f in ("dq", "dk", "dv"):
+            bufs[f].zero_()
+        _ = (bufs["q"].float() * 2).sum().item()  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, x in zip(("dq", "dk", "dv"), ref):
+            y = bufs[name]
+            assert torch.equal(x, y), f"replay {rep} {name}: max diff {(x.float() - y.float()).abs().max().item():.3e}"
+
+
 @pytest.mark.parametrize("softmax", [True, False])
 @pytest.mark.parametrize("shapes", [((16, 16, 516, 64), (2, 3, 200, 64)), ((2, 4, 700, 128), (1, 2, 90, 128))])
 def test_noalloc_equals_bwd_twice(cuda_device, softmax, shapes):
@@ -60,6 +93,21 @@ def test_noalloc_equals_bwd_twice(cuda_device, softmax, shapes):
             assert torch.isfinite(y).all(), name
             assert torch.equal(x, y), f"{name}: max diff {(x.float() - y.float()).abs().max().item():.3e}"
         assert ref[0].abs().sum() > 0
+
+
+def test_noalloc_at_max_rows(cuda_device):
+    """B * H * N = RBF_ATTN_NOALLOC_MAX_ROWS: the last entry of the array is
+    written and read; then a smaller call."""
+    sp = torch.cuda.current_stream(cuda_device).cuda_stream
+    for i, (B, H, N, D) in enumerate(((16, 64, 1024, 64), (1, 3, 333, 64))):
+        assert i == 1 or B * H * N == _lib.NOALLOC_MAX_ROWS
+        print(f"noalloc max rows call {i}: B={B} H={H} N={N} D={D}", flush=True)
+        bufs, a = make(B, H, N, D, torch.bfloat16, cuda_device, True, seed=40 + i)
+        ref, got = run_pair(bufs, a, sp)
+        for name, x, y in zip(("dq", "dk", "dv"), ref, got):
+            assert torch.equal(x, y), f"{name}: max diff {(x.float() - y.float()).abs().max().item():.3e}"
+        del bufs, ref, got
+        torch.cuda.empty_cache()
 
 
 def test_noalloc_rejects_oversize(cuda_device):
