@@ -220,8 +220,8 @@ int main(int argc, char** argv) {
   hip_check(hipEventCreate(&e1), "hipEventCreate");
   auto fwd = [&]() { abi_check(rbf_attn_fwd(&a, st), "rbf_attn_fwd"); };
   auto bwd = [&]() { abi_check(rbf_attn_bwd(&a, st), "rbf_attn_bwd"); };
-  auto dq = [&]() { abi_check(rbf_attn_bwd_stage(&a, st, 1), "rbf_attn_bwd_stage 1"); };
-  auto dkdv = [&]() { abi_check(rbf_attn_bwd_stage(&a, st, 2), "rbf_attn_bwd_stage 2"); };
+  auto stage1 = [&]() { abi_check(rbf_attn_bwd_stage(&a, st, 1), "rbf_attn_bwd_stage 1"); };
+  auto stage2 = [&]() { abi_check(rbf_attn_bwd_stage(&a, st, 2), "rbf_attn_bwd_stage 2"); };
   auto step = [&]() {
     fwd();
     bwd();
@@ -257,7 +257,7 @@ int main(int argc, char** argv) {
     return loop(fn, (int)n);
   };
   const double ms_fwd = kernel_loop(fwd), ms_bwd = kernel_loop(bwd);
-  const double ms_dq = kernel_loop(dq), ms_dkdv = kernel_loop(dkdv);
+  const double ms_dq = kernel_loop(stage1), ms_dkdv = kernel_loop(stage2);
   const int bwd_launches = rbf_attn_bwd_kernels(&a, nullptr);
 
   auto cold_median = [&](auto&& fn) {
