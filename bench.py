@@ -276,7 +276,8 @@ def setup_workload(w, dev):
 GRAPH_STEPS = 10  # steps per captured HIP graph (graph_step_us)
 
 
-def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold_reps: int, graph: bool):
+def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold_reps: int, graph: bool,
+                     kernel_s: float = 0.2, kernel_n: int = 200):
     """Step, per-kernel and cold-cache timings of one workload through the C
     ABI; returns (result dict, step ms)."""
     import torch
@@ -316,7 +317,7 @@ def measure_workload(w, dev, timer, steps: int, warmup: int, ramp_s: float, cold
     step_kernels = ("fwd", "bwd") if bwd_launches == 1 else ("fwd", "bwd_dq", "bwd_dkdv")
     calls = {"fwd": fwd, "bwd": bwd, "bwd_dq": stage(1), "bwd_dkdv": stage(2)}
     timed_kernels = step_kernels + (("bwd_dq", "bwd_dkdv") if bwd_launches == 1 else ())
-    kern_ms = {kname: timer.kernel_loop(calls[kname]) for kname in timed_kernels}
+    kern_ms = {kname: timer.kernel_loop(calls[kname], kernel_s, kernel_n) for kname in timed_kernels}
     for kname, t in kern_ms.items():
         log(f"  {kname}: {t * 1e3:.2f} us/launch" + ("" if kname in step_kernels else " (stage alone)"))
     kern_sum = sum(kern_ms[kk] for kk in step_kernels)
@@ -680,6 +681,9 @@ def main() -> int:
     ap.add_argument("--ramp-seconds", type=float, default=0.4,
                     help="untimed steps run for this long before the warmup steps (GPU clock ramp)")
     ap.add_argument("--cold-reps", type=int, default=25)
+    ap.add_argument("--kernel-seconds", type=float, default=0.2,
+                    help="each kernel's own timing loop runs at least this long ...")
+    ap.add_argument("--kernel-launches", type=int, default=200, help="... and at least this many launches")
     ap.add_argument("--workload", default="c2_model_bf16")
     ap.add_argument("--quick", action="store_true",
                     help="only the headline workload: no C3/C4 objects, reference sweep, train step or decode")
@@ -728,7 +732,7 @@ def main() -> int:
     # are its own timing loop's (what a profile of this run averages)
     peak_mb = peak_fwd_mb(dev, w)
     head, ms_step = measure_workload(w, dev, timer, args.steps, args.warmup, args.ramp_seconds, args.cold_reps,
-                                     graph=True)
+                                     graph=True, kernel_s=args.kernel_seconds, kernel_n=args.kernel_launches)
     result = {
         "metric": METRIC,
         "value": head["tflops"],
@@ -763,7 +767,8 @@ def main() -> int:
         for name in ("c3_long_bf16", "c4_nonsoftmax_bf16"):
             if name == w.name:
                 continue
-            r, _ = measure_workload(wl.CONFIGS[name], dev, timer, 20, 5, 0.2, 20, graph=False)
+            r, _ = measure_workload(wl.CONFIGS[name], dev, timer, 20, 5, 0.2, 20, graph=False,
+                                    kernel_s=args.kernel_seconds, kernel_n=args.kernel_launches)
             if not args.no_native:
                 r["native_harness"] = native_harness(name, 20, 5, 20, 0.2)
             result[name.split("_")[0]] = r
