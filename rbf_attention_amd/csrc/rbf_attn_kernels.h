@@ -1433,9 +1433,13 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
   const float* offg = p.lse + (int64_t)bh * N;
   const float* delg = SOFTMAX ? p.delta + (int64_t)bh * N : nullptr;
 
-  const int blk0 = nblk - (ngrp - grp) * GB;
+  // Key groups are aligned to the start of the sequence (group g holds blocks
+  // [g GB, g GB + GB)): the heaviest causal group is then a full one, and the
+  // one group that may hold fewer real blocks is the lightest (aligned to the
+  // end, it was the heaviest, with most of its waves idle).
+  const int blk0 = grp * GB;
   const int kblk0 = blk0 + wave * KPW;
-  const bool wave_on = kblk0 + KPW - 1 >= 0;
+  const bool wave_on = kblk0 < nblk;
 
   int k0[KPW], ktok[KPW], ilo[KPW];
   frag kf[KPW][KS], vf[KPW][KS];
@@ -1445,7 +1449,7 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
     k0[j] = org + 32 * (kblk0 + j);
     ktok[j] = k0[j] + n;
     ilo[j] = first_query(ktok[j], causal, npre);
-    const bool kvalid = wave_on && ktok[j] >= 0;
+    const bool kvalid = wave_on && ktok[j] >= 0 && ktok[j] < N;
     float s = 0.f;
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
@@ -1703,7 +1707,7 @@ __device__ __forceinline__ void rbf_bwd_dkdv_group(const Params& p, int bh, int 
 #pragma unroll
   for (int j = 0; j < KPW; ++j) {
     const float cs = xhalf_sum(csum[j]);
-    if (ktok[j] < 0) continue;
+    if (ktok[j] < 0 || ktok[j] >= N) continue;
     T* dkrow = dK + (int64_t)ktok[j] * p.sdk[2];
     T* dvrow = dV + (int64_t)ktok[j] * p.sdv[2];
     const T* krow = K + (int64_t)ktok[j] * p.sk[2];
@@ -1798,9 +1802,10 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
   const float* offg = p.lse + (int64_t)bh * N;
   const float* delg = SOFTMAX ? p.delta + (int64_t)bh * N : nullptr;
 
-  const int blk0 = nblk - (ngrp - grp) * NP;
+  // start-aligned key groups, as in rbf_bwd_dkdv_group
+  const int blk0 = grp * NP;
   const int kblk = blk0 + j;
-  const bool wave_on = kblk >= 0;
+  const bool wave_on = kblk < nblk;
   const int k0 = org + 32 * kblk;
   const int ktok = k0 + n;
   const bool kvalid = wave_on && ktok >= 0;
