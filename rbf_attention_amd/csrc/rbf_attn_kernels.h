@@ -564,15 +564,15 @@ struct TileLayout {
 };
 
 // ---------------------------------------------------------------------------
-// LDS-DMA staging of chunk-major tiles (16-bit elements, 128 features).
+// LDS-DMA staging of chunk-major tiles (16-bit elements, 64 or 128 features).
 //
 // global_load_lds_dwordx4 writes each lane's 16 bytes to consecutive 16-byte
 // LDS slots (M0 base + 16 * lane), i.e. 1 KB per instruction: in a CLayout
 // tile, 64 consecutive rows of one chunk column.  So one instruction stages
 // rows r0 .. r0 + 63 of chunk ch, lane l reading row r0 + l, and no register
-// ever holds the tile.  Rows outside [0, N) read row 0 or N - 1 instead: the
-// kernels mask such keys and queries by their -inf norm or offset, never by
-// their values, which only have to be finite.
+// ever holds the tile.  Rows outside [0, N) read zeros (the buffer range
+// check of buffer_rsrc): the kernels mask such keys and queries by their -inf
+// norm or offset, never by their values, which only have to be finite.
 //
 // A pipeline of three tiles (dma_pipeline) runs the compute of tile t while
 // tile t + 1 is landed in LDS (its per-row terms formed from LDS) and tile
@@ -899,7 +899,7 @@ __device__ inline typename Elem<T>::frag ones_row_frag(int n) {
 constexpr float kBoundMargin = 60.f;  // P <= 2^60 under the static bound
 constexpr float kSumLow = 0x1p-60f, kSumHigh = 0x1p100f;
 
-// DMA: K and V tiles staged by LDS-DMA (dma_pipeline; 16-bit, D = 128 only)
+// DMA: K and V tiles staged by LDS-DMA (dma_pipeline; 16-bit, D = 64 or 128)
 // instead of through registers.
 template <typename T, int DP, int W, int BN, bool SOFTMAX, bool DMA = false>
 __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) {
@@ -1121,7 +1121,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) v
 //   S^T = K Q^T (init -0.5||k||^2), P = exp2(c S^T - L),
 //   dP^T = V dO^T (init -Delta), dS = P dP^T, dQ^T += K^T dS^T.
 // ---------------------------------------------------------------------------
-// DMA: K and V tiles staged by LDS-DMA (dma_pipeline; 16-bit, D = 128 only)
+// DMA: K and V tiles staged by LDS-DMA (dma_pipeline; 16-bit, D = 64 or 128)
 // instead of through registers.
 template <typename T, int DP, int W, int QPW, int BN, bool SOFTMAX, bool EARLY = true, bool DMA = false>
 __device__ __forceinline__ void rbf_bwd_dq_group(const Params& p, int bh, int grp) {
@@ -1760,7 +1760,7 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
 // reads before its MFMAs (sched_group_barrier), trading registers for hidden
 // LDS latency.
 // ---------------------------------------------------------------------------
-// DMA: Q and dO tiles staged by LDS-DMA (dma_pipeline; D = 128 only), the
+// DMA: Q and dO tiles staged by LDS-DMA (dma_pipeline; the launcher uses it at D = 128), the
 // per-query offsets through two registers of the first wave.
 template <typename T, int DP, int NP, int BM, bool SOFTMAX, bool SGB = false, bool DMA = false>
 __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh, int grp) {
