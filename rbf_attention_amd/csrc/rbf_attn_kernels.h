@@ -872,9 +872,12 @@ __device__ inline f32x16_t splat16(float x) {
 //   P   = exp2(c S^T - m),
 //   O^T += V^T P^T with P rounded to the element type (as the reference
 //   rounds it before its P V product, rbf_attention.py:201),
-//   l_r += 1^T P^T on the same MFMA path (an operand whose first row is
-//   ones): O is normalised by the sum of exactly the rounded P its numerator
-//   uses, so a row that sees one key returns that key's v exactly;
+//   l_r += the rounded P's sum, in fp32 (this streaming forward: v_dot2
+//   against ones on the VALU, 2 MFMAs per block fewer, C3 forward 1140 ->
+//   1128 us; the head-resident forward: 1^T P^T on the MFMA path, through an
+//   operand whose first row is ones): O is normalised by the sum of exactly
+//   the rounded P its numerator uses, so a row that sees one key returns that
+//   key's v exactly;
 //   l += sum_j P in fp32 from the unrounded P, for L (the reference sums the
 //   unrounded P, 196-198).  L taken from l_r was off by up to 2^-9 relative
 //   per row, a scale every P of the backward then carried (dV's error at
@@ -962,10 +965,14 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
     qn2 += sumsq8<T>(qf[t]);
   }
   qn2 = c * 0.5f * xhalf_sum(qn2);
-  const frag onesA = ones_row_frag<T>(n);
+  frag ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (T)1.f;
 
-  f32x16_t oacc[ND], lacc;  // lacc row 0: sum of the rounded P
-  float lrow;  // this lane's share (16 of a block's 32 keys) of the unrounded P's sum
+  f32x16_t oacc[ND];
+  // this lane's share (16 of a block's 32 keys) of the sums of the rounded P
+  // (normalises O) and of the unrounded P (gives L)
+  float lrnd, lrow;
   float m_run;
 
   typedef TileFor<T, BN, DP, NT> TileT;
@@ -981,7 +988,7 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
     constexpr bool SAFE = decltype(safe_tag)::value;
 #pragma unroll
     for (int d = 0; d < ND; ++d) oacc[d] = zero16();
-    lacc = zero16();
+    lrnd = 0.f;
     lrow = 0.f;
     m_run = !SOFTMAX ? qn2 : (SAFE ? -__builtin_inff() : qn2 - kBoundMargin);
     // The blocks of key tile kt against this wave's queries, from tiles kbuf
@@ -1016,7 +1023,7 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
             const float alpha = (mnew == -__builtin_inff()) ? 1.f : fast_exp2(m_run - mnew);
 #pragma unroll
             for (int d = 0; d < ND; ++d) oacc[d] *= alpha;
-            lacc *= alpha;
+            lrnd *= alpha;
             lrow *= alpha;
             m_run = mnew;
           }
@@ -1034,8 +1041,8 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
         for (int t = 0; t < 2; ++t) {
 #pragma unroll
           for (int d = 0; d < ND; ++d) oacc[d] = E::mma(vA[d][t], pf[t], oacc[d]);
-          if constexpr (SOFTMAX) lacc = E::mma(onesA, pf[t], lacc);
         }
+        if constexpr (SOFTMAX) lrnd += dot8<T>(pf[0], ones) + dot8<T>(pf[1], ones);
       }
     };
     if constexpr (DMA) {
@@ -1081,9 +1088,7 @@ __device__ __forceinline__ void rbf_fwd_group(const Params& p, int bh, int grp) 
   }
 
   if (!wave_on) return;
-  // lacc row 0 (element 0 of the h = 0 lanes) is the rounded P's sum; the
-  // h = 1 lanes hold row 4, which is zero.
-  const float inv = SOFTMAX ? 1.f / xhalf_sum(lacc[0]) : 1.f;
+  const float inv = SOFTMAX ? 1.f / xhalf_sum(lrnd) : 1.f;
   const float lsum = SOFTMAX ? xhalf_sum(lrow) : 1.f;
   if (qtok < 0) return;
   T* orow = O + (int64_t)qtok * p.so[2];
