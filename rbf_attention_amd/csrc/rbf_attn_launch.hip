@@ -161,16 +161,22 @@ constexpr int kHrBlocks64 = kHrMaxBlocks;  // D <= 64: N <= 576
 
 // LDS-DMA tile staging (16-bit, D = 64 or 128 filling the padded width DP:
 // the streaming kernels' tiles go from global memory straight into LDS, three
-// tiles in flight), for operands whose rows dma_rows_ok admits
-// (rbf_attn_staging.h); others take the register-staged kernels.
+// tiles in flight), when the rows of both operands a kernel stages are ones
+// dma_rows_ok admits (rbf_attn_staging.h); otherwise the kernel is the
+// register-staged one.  Each kernel checks only what it stages: the forward
+// and dQ kernels stage K and V (and read Q and dO directly), the dK/dV kernels
+// Q and dO (and read K and V directly); a forward's dO descriptor is unset.
 // RBF_ATTN_DMA=0 keeps the register-staged kernels for every shape.
-bool use_dma(const Params& p, int dp) {
+bool dma_pair_ok(const Params& p, int dp, int64_t stride_a, int64_t stride_b) {
   static const int forced = env_choice("RBF_ATTN_DMA");
   constexpr int64_t esz = sizeof(Elt);
-  return !kIsF32 && forced != 0 && p.D == dp && dma_rows_ok(p.N, p.sk[2], p.D, esz) &&
-         dma_rows_ok(p.N, p.sv[2], p.D, esz) && dma_rows_ok(p.N, p.sq[2], p.D, esz) &&
-         dma_rows_ok(p.N, p.sdo[2], p.D, esz);
+  return !kIsF32 && forced != 0 && p.D == dp && dma_rows_ok(p.N, stride_a, p.D, esz) &&
+         dma_rows_ok(p.N, stride_b, p.D, esz);
 }
+// K and V tiles: the forward and dQ kernels.
+bool use_dma_kv(const Params& p, int dp) { return dma_pair_ok(p, dp, p.sk[2], p.sv[2]); }
+// Q and dO tiles: the dK/dV kernels.
+bool use_dma_qdo(const Params& p, int dp) { return dma_pair_ok(p, dp, p.sq[2], p.sdo[2]); }
 
 template <int DP, bool SM, int W, int BN, bool BIN = false, bool DMA = false>
 hipError_t fwd_cfg(const Params& p, hipStream_t st) {
@@ -236,7 +242,7 @@ hipError_t fwd_default(const Params& p, hipStream_t st) {
     // B63 H8 N1028 149 -> 131, B20 H8 N700 30.4 -> 27.9, B16 H8 N2052 118 ->
     // 108, B15 H8 N4100 382 -> 344, B4 H8 N8196 354 -> 346 (8 waves over
     // 128-key tiles: 374 and 358); B16 H8 N1028 37.8 -> 39.4.
-    if (DP == 64 && use_dma(p, DP)) return fwd_cfg<DP, SM, 4, 64, false, true>(p, st);
+    if (DP == 64 && use_dma_kv(p, DP)) return fwd_cfg<DP, SM, 4, 64, false, true>(p, st);
     // Register staging (padded head dims, or strides past the DMA range): one
     // group per work-group, 4 waves over 64-key tiles up to N = 8192.
     // Measured against the binned forms at D = 48 (bf16 softmax fwd, us): B63
@@ -245,7 +251,7 @@ hipError_t fwd_default(const Params& p, hipStream_t st) {
     if (p.N >= 4 * kLongSeq) return bins_fit(p) ? fwd_cfg<DP, SM, 8, 128, true>(p, st) : fwd_cfg<DP, SM, 8, 128>(p, st);
     return fwd_cfg<DP, SM, 4, 64>(p, st);
   } else {
-    if (use_dma(p, DP)) return bins_fit(p) ? fwd_cfg<DP, SM, 8, 64, true, true>(p, st) : fwd_cfg<DP, SM, 8, 64, false, true>(p, st);
+    if (use_dma_kv(p, DP)) return bins_fit(p) ? fwd_cfg<DP, SM, 8, 64, true, true>(p, st) : fwd_cfg<DP, SM, 8, 64, false, true>(p, st);
     return bins_fit(p) ? fwd_cfg<DP, SM, 8, 64, true>(p, st) : fwd_cfg<DP, SM, 8, 64>(p, st);
   }
 }
@@ -271,7 +277,7 @@ hipError_t dq_default(const Params& p, hipStream_t st) {
     // forward: against the binned form (bf16 softmax dQ, us) B63 H8 N1028 192
     // -> 168, B16 H8 N1028 45.0 -> 43.2, B20 H8 N700 33.5 -> 31.4, B16 H8
     // N2052 140 -> 126, B15 H8 N4100 491 -> 419, B4 H8 N8196 450 -> 414.
-    if (DP == 64 && use_dma(p, DP)) return dq_cfg<DP, SM, 4, 1, 64, true, false, true>(p, st);
+    if (DP == 64 && use_dma_kv(p, DP)) return dq_cfg<DP, SM, 4, 1, 64, true, false, true>(p, st);
     // register staging: one group per work-group (D = 48: 1.0-4.7 % faster
     // than binned at N = 700-8196)
     return dq_cfg<DP, SM, 4, 1, 128>(p, st);
@@ -282,7 +288,7 @@ hipError_t dq_default(const Params& p, hipStream_t st) {
     // form (bf16 softmax dQ): B63 H16 N516 302 -> 258 us, B8 H16 N516 36.5 ->
     // 33.2, B31 H16 N1028 363 -> 344; slower from N = 1500 (73 -> 80).
     if (p.N < 1200) return dq_cfg<DP, SM, 4, 1, 32, false>(p, st);
-    if (use_dma(p, DP))
+    if (use_dma_kv(p, DP))
       return bins_fit(p) ? dq_cfg<DP, SM, 8, 1, 64, true, true, true>(p, st) : dq_cfg<DP, SM, 8, 1, 64, true, false, true>(p, st);
     return bins_fit(p) ? dq_cfg<DP, SM, 8, 1, 32, true, true>(p, st) : dq_cfg<DP, SM, 8, 1, 32>(p, st);
   }
@@ -310,7 +316,7 @@ hipError_t dkdv_default(const Params& p, hipStream_t st) {
     // fast or slower with it (C4 188 -> 191 us), at N = 8192 faster (605 -> 589).
     // With it, one group per work-group (as the forward and dQ): 0.7-3.4 %
     // faster than the binned form at B15 H8 N4100, B4 H8 N8196, B2 H8 N16388.
-    if (DP == 64 && p.N >= 2 * kLongSeq && use_dma(p, DP))
+    if (DP == 64 && p.N >= 2 * kLongSeq && use_dma_qdo(p, DP))
       return dkdv_cfg<DP, SM, 8, 1, 128, true, false, false, false, true>(p, st);
     // Register staging: one group per work-group, 4 waves below N = 4096 and 8
     // above.  Against the binned forms at D = 48 (bf16 softmax dK/dV, us): B63
@@ -324,7 +330,7 @@ hipError_t dkdv_default(const Params& p, hipStream_t st) {
     // form (bf16 softmax dK/dV): B32 H8 N516 156 -> 114 us, B63 H16 N516 657
     // -> 470, B31 H16 N1028 891 -> 562 (DMA; 585 without), B4 H16 N1500 193
     // -> 114; at B2 H8 N300 18.5 against 18.8.
-    if (p.N >= 1024 && use_dma(p, DP)) return dkdv_pair_cfg<DP, SM, 4, 64, true, false, true>(p, st);
+    if (p.N >= 1024 && use_dma_qdo(p, DP)) return dkdv_pair_cfg<DP, SM, 4, 64, true, false, true>(p, st);
     return dkdv_pair_cfg<DP, SM, 4, 64, true>(p, st);
   }
 }
@@ -343,11 +349,11 @@ hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
     case 4: return fwd_cfg<DP, SM, 2, 64>(p, st);
     case 5: return fwd_cfg<DP, SM, 4, 32>(p, st);
     case 6:
-      if (use_dma(p, DP)) return fwd_cfg<DP, SM, 4, 64, false, true>(p, st);
+      if (use_dma_kv(p, DP)) return fwd_cfg<DP, SM, 4, 64, false, true>(p, st);
       break;
     case 7: return fwd_cfg<DP, SM, 4, 64, true>(p, st);
     case 8:
-      if (use_dma(p, DP)) return fwd_cfg<DP, SM, 8, DP == 64 ? 128 : 64, false, true>(p, st);
+      if (use_dma_kv(p, DP)) return fwd_cfg<DP, SM, 8, DP == 64 ? 128 : 64, false, true>(p, st);
       break;
     case 10:
       if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return hr_fwd(p, SM, 8, st); }
@@ -373,7 +379,7 @@ hipError_t dq_any_cfg(const Params& p, hipStream_t st) {
       case 10: return dq_cfg<DP, SM, 8, 1, 32>(p, st);
       case 11: return dq_cfg<DP, SM, 8, 1, 32, false>(p, st);
       case 14:
-        if (use_dma(p, DP)) return dq_cfg<DP, SM, 8, 1, 64, true, false, true>(p, st);
+        if (use_dma_kv(p, DP)) return dq_cfg<DP, SM, 8, 1, 64, true, false, true>(p, st);
         break;
       default: break;
     }
@@ -391,7 +397,7 @@ hipError_t dq_any_cfg(const Params& p, hipStream_t st) {
     case 8: return dq_cfg<DP, SM, 4, 1, 128>(p, st);
     case 11: return dq_cfg<DP, SM, 8, 1, 64>(p, st);
     case 12:
-      if (use_dma(p, DP)) return dq_cfg<DP, SM, 4, 1, 64, true, false, true>(p, st);
+      if (use_dma_kv(p, DP)) return dq_cfg<DP, SM, 4, 1, 64, true, false, true>(p, st);
       break;
     case 13: return dq_cfg<DP, SM, 4, 1, 64, true, true>(p, st);
     default: break;

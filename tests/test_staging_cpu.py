@@ -60,11 +60,35 @@ def test_dma_rows_rule(driver):
     assert got == [want for _, want in CASES], list(zip(CASES, got))
 
 
+def _functions(src):
+    """Launcher source split into (name, body) per `hipError_t name(` definition."""
+    import re
+
+    marks = [(m.start(), m.group(1)) for m in re.finditer(r"\nhipError_t (\w+)\(", src)]
+    return [(name, src[a : (marks[i + 1][0] if i + 1 < len(marks) else len(src))]) for i, (a, name) in enumerate(marks)]
+
+
 def test_launchers_use_the_rule():
     """Every LDS-DMA decision of the launchers goes through dma_rows_ok for
-    all four staged operands (q, k, v, dout)."""
+    both operands the chosen kernel stages: K and V (forward, dQ), Q and dO
+    (dK/dV).  A forward's dO is unset, so it must not be checked there."""
     src = open(os.path.join(CSRC, "rbf_attn_launch.hip")).read()
-    body = src[src.index("bool use_dma("):]
+    body = src[src.index("bool dma_pair_ok("):]
     body = body[: body.index("\n}\n")]
-    for stride in ("p.sk[2]", "p.sv[2]", "p.sq[2]", "p.sdo[2]"):
-        assert f"dma_rows_ok(p.N, {stride}, p.D, esz)" in body
+    assert "dma_rows_ok(p.N, stride_a, p.D, esz)" in body and "dma_rows_ok(p.N, stride_b, p.D, esz)" in body
+    assert "use_dma_kv(const Params& p, int dp) { return dma_pair_ok(p, dp, p.sk[2], p.sv[2]); }" in src
+    assert "use_dma_qdo(const Params& p, int dp) { return dma_pair_ok(p, dp, p.sq[2], p.sdo[2]); }" in src
+    assert "use_dma(" not in src
+    calls = "\n".join(l for l in src.split("\n") if not l.startswith("bool use_dma_"))  # drop the definitions
+    seen = set()
+    for name, fn in _functions(calls):
+        kv, qdo = "use_dma_kv(" in fn, "use_dma_qdo(" in fn
+        if name.startswith(("fwd_", "dq_")):
+            assert not qdo, name
+            seen.add(name) if kv else None
+        elif name.startswith("dkdv_"):
+            assert not kv, name
+            seen.add(name) if qdo else None
+        else:
+            assert not (kv or qdo), name
+    assert {"fwd_default", "dq_default", "dkdv_default"} <= seen, seen
