@@ -1866,8 +1866,13 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
       bool act[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) act[qb] = wave_on && blk_any(org + 32 * (qblk0 + qb), k0, causal, npre);
+      // Each role runs at a raised issue priority in the phase where its path
+      // is the longer one (the P-wave's S chain, exponentials and P stores;
+      // the dS-wave's P read, dS and dK), so that the other wave's MFMAs fill
+      // its gaps rather than delay it: C3 dK/dV 2277 -> 2254 us.
       if constexpr (PW) {
         // phase 1: S, P -> registers and LDS
+        __builtin_amdgcn_s_setprio(2);
         frag pf[QB][2];
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
@@ -1891,6 +1896,7 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
 #pragma unroll
           for (int u = 0; u < 4; ++u) sP[j][qb][u][lane] = pv[u];
         }
+        __builtin_amdgcn_s_setprio(0);
         if constexpr (DMA) lds_barrier();
         else __syncthreads();
         // phase 2: dV^T += dO^T P
@@ -1926,6 +1932,7 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
         }
         if constexpr (DMA) lds_barrier();
         else __syncthreads();
+        __builtin_amdgcn_s_setprio(2);
         // phase 2: dS = P dP, dK^T += Q^T dS
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
@@ -1951,6 +1958,7 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
             __builtin_amdgcn_sched_group_barrier(0x008, 2 * ND, 0);
           }
         }
+        __builtin_amdgcn_s_setprio(0);
       }
     };
     if constexpr (DMA) {
