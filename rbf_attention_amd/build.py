@@ -51,6 +51,10 @@ COMMON_FLAGS = [
 # 487 us per step).
 HR_FLAGS = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
 STREAM_FLAGS = ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
+# The bf16 dQ kernels (their own unit, RBF_PART=2) run faster with the
+# occupancy-targeting iterative scheduler: C3 dQ 1571 -> 1543 us, C4 dQ
+# 136.0 -> 135.3 us, where the forward and dK/dV kernels lose 1-2 % with it.
+DQ_FLAGS = ["-mllvm", "-amdgpu-sched-strategy=iterative-maxocc"]
 # MFMA accumulators are kept in ordinary VGPRs (the VGPR form of the MFMA
 # instructions), so the softmax VALU work reads them without AGPR<->VGPR
 # copies.  Every unit but the fp32 one with 256 features (RBF_WIDE), whose
@@ -78,7 +82,8 @@ def build(verbose: bool = True) -> str:
     hipcc = _hipcc()
     units = [
         ("rbf_attn_capi.hip", VGPR_FORM),
-        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=0", *STREAM_FLAGS, *VGPR_FORM]),
+        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=0", "-DRBF_PART=1", *STREAM_FLAGS, *VGPR_FORM]),
+        ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=0", "-DRBF_PART=2", *DQ_FLAGS, *VGPR_FORM]),
         ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=1", *STREAM_FLAGS, *VGPR_FORM]),
         ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=2", *STREAM_FLAGS, *VGPR_FORM]),
         ("rbf_attn_launch.hip", ["-DRBF_ELEM_ID=2", "-DRBF_WIDE", *STREAM_FLAGS]),

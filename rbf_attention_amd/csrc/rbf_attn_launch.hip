@@ -21,6 +21,17 @@
 #if defined(RBF_WIDE) && RBF_ELEM_ID != 2
 #error "RBF_WIDE builds the fp32 kernels with 256 features only"
 #endif
+// RBF_PART splits an element type's launchers over two units, so that the
+// dQ kernels can be compiled with a machine-scheduler strategy of their own:
+// 0 (default) every launcher; 1 all but dQ (the whole backward calls the
+// other unit's launch_bwd_dq_*); 2 the dQ launcher only.  Each kernel is
+// instantiated in one unit.
+#ifndef RBF_PART
+#define RBF_PART 0
+#endif
+#if RBF_PART != 0 && defined(RBF_WIDE)
+#error "RBF_PART applies to the per-element-type units"
+#endif
 
 namespace rbf {
 namespace {
@@ -474,6 +485,7 @@ hipError_t decode_dp(const DecodeParams& p, hipStream_t st) {
 // and accumulators exceed the 512 registers of a lane, and with the VGPR form
 // of the MFMA instructions forced (as for every other kernel) the compiler
 // fails on them, so that unit leaves the register classes to the compiler.
+#if RBF_PART != 2
 hipError_t fwd_256(const Params& p, bool sm, hipStream_t st) {
 #if RBF_ELEM_ID == 2
   return launch_fwd_wide_fp32(p, sm ? 0 : 1, st);
@@ -481,6 +493,8 @@ hipError_t fwd_256(const Params& p, bool sm, hipStream_t st) {
   return sm ? fwd_default<256, true>(p, st) : fwd_default<256, false>(p, st);
 #endif
 }
+#endif
+#if RBF_PART != 1
 hipError_t dq_256(const Params& p, bool sm, hipStream_t st) {
 #if RBF_ELEM_ID == 2
   return launch_bwd_dq_wide_fp32(p, sm ? 0 : 1, st);
@@ -488,6 +502,8 @@ hipError_t dq_256(const Params& p, bool sm, hipStream_t st) {
   return sm ? dq_default<256, true>(p, st) : dq_default<256, false>(p, st);
 #endif
 }
+#endif
+#if RBF_PART != 2
 hipError_t dkdv_256(const Params& p, bool sm, hipStream_t st) {
 #if RBF_ELEM_ID == 2
   return launch_bwd_dkdv_wide_fp32(p, sm ? 0 : 1, st);
@@ -495,6 +511,7 @@ hipError_t dkdv_256(const Params& p, bool sm, hipStream_t st) {
   return sm ? dkdv_default<256, true>(p, st) : dkdv_default<256, false>(p, st);
 #endif
 }
+#endif
 
 // Head dim D (a multiple of 8 in [8, 256]) runs on the kernel for the next
 // padded width DP in {32, 64, 128, 256}; features D..DP-1 are zero-filled (as
@@ -509,8 +526,11 @@ hipError_t dkdv_256(const Params& p, bool sm, hipStream_t st) {
     return W256(p, sm, st);                                                         \
   } while (0)
 
-hipError_t fwd_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(fwd_default, fwd_any_cfg, fwd_256); }
+#if RBF_PART != 1
 hipError_t dq_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(dq_default, dq_any_cfg, dq_256); }
+#endif
+#if RBF_PART != 2
+hipError_t fwd_any(const Params& p, int variant, hipStream_t st) { RBF_DISPATCH(fwd_default, fwd_any_cfg, fwd_256); }
 hipError_t dkdv_any(const Params& p, int variant, hipStream_t st) {
   RBF_DISPATCH(dkdv_default, dkdv_any_cfg, dkdv_256);
 }
@@ -534,7 +554,12 @@ bool bwd_one_launch(const Params& p) {
 
 hipError_t bwd_any(const Params& p, int variant, hipStream_t st) {
   if (bwd_one_launch(p)) return hr_bwd(p, variant == 0, st);
+#if RBF_PART == 1
+  static_assert(RBF_ELEM_ID == 0, "the split build is for bf16");
+  hipError_t e = launch_bwd_dq_bf16(p, variant, st);
+#else
   hipError_t e = dq_any(p, variant, st);
+#endif
   if (e != hipSuccess) return e;
   return dkdv_any(p, variant, st);
 }
@@ -550,6 +575,10 @@ hipError_t decode_any(const DecodeParams& p, int variant, hipStream_t st) {
   return sm ? decode_dp<256, true>(p, st) : decode_dp<256, false>(p, st);
 #endif
 }
+#endif  // RBF_PART != 2
+#ifdef RBF_DISPATCH
+#undef RBF_DISPATCH
+#endif
 #endif  // !RBF_WIDE
 
 }  // namespace
@@ -579,11 +608,14 @@ hipError_t launch_decode_wide_fp32(const DecodeParams& p, int variant, hipStream
 #define RBF_CAT2(a, b) a##b
 #define RBF_CAT(a, b) RBF_CAT2(a, b)
 
-hipError_t RBF_CAT(launch_fwd_, RBF_NAME)(const Params& p, int variant, hipStream_t st) {
-  return fwd_any(p, variant, st);
-}
+#if RBF_PART != 1
 hipError_t RBF_CAT(launch_bwd_dq_, RBF_NAME)(const Params& p, int variant, hipStream_t st) {
   return dq_any(p, variant, st);
+}
+#endif
+#if RBF_PART != 2
+hipError_t RBF_CAT(launch_fwd_, RBF_NAME)(const Params& p, int variant, hipStream_t st) {
+  return fwd_any(p, variant, st);
 }
 hipError_t RBF_CAT(launch_bwd_dkdv_, RBF_NAME)(const Params& p, int variant, hipStream_t st) {
   return dkdv_any(p, variant, st);
@@ -595,6 +627,7 @@ int RBF_CAT(bwd_kernels_, RBF_NAME)(const Params& p) { return bwd_one_launch(p) 
 hipError_t RBF_CAT(launch_decode_, RBF_NAME)(const DecodeParams& p, int variant, hipStream_t st) {
   return decode_any(p, variant, st);
 }
+#endif  // RBF_PART != 2
 #endif  // RBF_WIDE
 
 }  // namespace rbf
