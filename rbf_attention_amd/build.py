@@ -3,7 +3,8 @@
 Usage:  python -m rbf_attention_amd.build      (or build() from Python)
 
 The library lands next to this file, so it travels with the source tree.
-Each element type's kernels are a separate translation unit, compiled in
+Each element type's kernels are a separate translation unit (bf16's two: the
+dQ launcher and the rest, for their scheduler strategies), compiled in
 parallel, then linked with the C ABI into one shared object.
 """
 from __future__ import annotations

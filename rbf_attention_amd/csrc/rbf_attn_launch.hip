@@ -1,7 +1,8 @@
 // Launchers for one element type.  Compiled once per dtype with
 // -DRBF_ELEM_ID=0 (bf16), 1 (fp16) or 2 (fp32), so the three instantiation
-// sets build in parallel; once more with -DRBF_ELEM_ID=2 -DRBF_WIDE for the
-// fp32 kernels with 256 features (launch_*_wide_fp32).
+// sets build in parallel (bf16 as two units, RBF_PART below); once more with
+// -DRBF_ELEM_ID=2 -DRBF_WIDE for the fp32 kernels with 256 features
+// (launch_*_wide_fp32).
 //
 // A kernel configuration is (W waves per work-group, blocks of 32 tokens per
 // wave, LDS tile of streamed tokens).  Defaults per padded head dim DP are in
