@@ -461,7 +461,20 @@ __device__ __forceinline__ void bwd_dkdv_hr_body(const Params& p, T* sQ, T* sD, 
     }
   };
   int kb = hr_block(0, wave, W, nblk, false);
-  load_kv(kb);
+  if constexpr (XFER && !POS) {
+    // After a dQ pass, sQ / sD still hold the head's K and V (tokens outside
+    // [0, N) and features past D as zeros) until the barrier below: the first
+    // key block comes from there instead of from global memory (C2 backward
+    // 56.15 -> 55.4 us).  With a position term that pass's K tile holds k + P,
+    // so the block is loaded as raw K here.
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      kf[t] = kb >= 0 ? ld8<T>(sQ + L::off(32 * kb + n, 16 * t + 8 * h)) : zero_frag<T>();
+      vf[t] = kb >= 0 ? ld8<T>(sD + L::off(32 * kb + n, 16 * t + 8 * h)) : zero_frag<T>();
+    }
+  } else {
+    load_kv(kb);
+  }
 
   // L and Delta of the rows this thread stages are requested with the Q / dO
   // rows, so the load phase waits for one round trip.
