@@ -1766,9 +1766,10 @@ __global__ __launch_bounds__(64 * W) void rbf_bwd_dkdv_kernel(const Params p) {
 // form dS: dS and its column sum then carry no rounding of P, which only the
 // dV product sees (rounded to the element type, as in the reference).  With P
 // handed over in the element type instead, dK's relative L2 error at C3 was
-// 1.25x that of the reference's own rounding.  SGB: every 32-query block issues all of its LDS operand
-// reads before its MFMAs (sched_group_barrier), trading registers for hidden
-// LDS latency.
+// 1.25x that of the reference's own rounding.  SGB: every 32-query block
+// issues its LDS operand reads ahead of its MFMAs (sched_group_barrier: all
+// of them before the S / dP products, in two halves before the dV / dK
+// products), trading registers for hidden LDS latency.
 // ---------------------------------------------------------------------------
 // DMA: Q and dO tiles staged by LDS-DMA (dma_pipeline; the launcher uses it at D = 128), the
 // per-query offsets through two registers of the first wave.
@@ -1914,8 +1915,12 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
             for (int t = 0; t < 2; ++t)
               acc[d] = E::mma(TLy::tr(sDb, 32 * qb + 16 * t, 32 * d, lane), pf[qb][t], acc[d]);
           if constexpr (SGB) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 4 * ND, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 2 * ND, 0);
+            // in two halves: C3 dK/dV -2.0 % against all reads before all
+            // MFMAs (quarters: -0.4 %, two reads per MFMA: +0.1 %)
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * ND, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, ND, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * ND, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, ND, 0);
           }
         }
       } else {
@@ -1959,8 +1964,12 @@ __device__ __forceinline__ void rbf_bwd_dkdv_pair_group(const Params& p, int bh,
             for (int t = 0; t < 2; ++t)
               acc[d] = E::mma(TLy::tr(sQb, 32 * qb + 16 * t, 32 * d, lane), sf[t], acc[d]);
           if constexpr (SGB) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 4 * ND, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 2 * ND, 0);
+            // in two halves: C3 dK/dV -2.0 % against all reads before all
+            // MFMAs (quarters: -0.4 %, two reads per MFMA: +0.1 %)
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * ND, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, ND, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * ND, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, ND, 0);
           }
         }
         __builtin_amdgcn_s_setprio(0);
