@@ -182,15 +182,19 @@ __device__ inline int hr_block(int k, int wave, int W, int nblk, bool reverse) {
 // Forward, head-resident.  The work-group loads the head's K and V (and
 // -0.5||k||^2) into LDS once; wave w then computes the output of its query
 // blocks as rbf_fwd_group does per block (static softmax bound; O normalised
-// by the rounded P's sum from the MFMA path, L from the unrounded P's fp32
-// sum; online max for fp16, or as a per-block rerun when a row's sum leaves
-// [2^-60, 2^100]), reading K rows and transposed V from the resident tiles.
+// by the rounded P's fp32 sum, L from the unrounded P's; online max for fp16,
+// or as a per-block rerun when a row's sum leaves [2^-60, 2^100]), reading K
+// rows and transposed V from the resident tiles.
 //
-// Without a running max (static bound, non-softmax) the key loop is software
-// pipelined: iteration kb issues the S MFMAs of block kb+1 (K fragments and
-// norms read one block earlier) next to the exponentials of block kb, so the
-// MFMA and VALU work of one wave overlap.  Only the causal diagonal block
-// needs a mask; it is peeled off the loop.
+// With up to 12 waves and no running max (non-softmax) the key loop is
+// software pipelined: iteration kb issues the S MFMAs of block kb+1 (K
+// fragments and norms read one block earlier) next to the exponentials of
+// block kb, so the MFMA and VALU work of one wave overlap.  Only the causal
+// diagonal block needs a mask; it is peeled off the loop.  The softmax forward
+// runs 16 waves (4 per SIMD) with the plain loop instead: its registers fit
+// 128 per lane only without the pipeline's second S accumulator and norm rows,
+// and the other waves on the SIMD do the overlapping (C2 forward 22.9 -> 22.4
+// us against 12 pipelined waves; fp16 24.1 -> 23.5).
 // ---------------------------------------------------------------------------
 template <typename T, int DP, int W, int NB, bool SOFTMAX, bool POS = false>
 __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
@@ -256,7 +260,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
     return s;
   };
 
-  const frag onesA = ones_row_frag<T>(n);
+  const frag ones = ones_frag<T>();
   for (int k = 0; qb >= 0; ++k) {
     // the next block's Q fragments are requested before this block's work
     const int qb_next = hr_block(k + 1, wave, W, nblk, causal);
@@ -272,10 +276,12 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
     // key blocks [0, kend) hold every key some query of the block sees
     const int kend = causal ? min(nblk, ((max(q0 + 31, npre - 1) - org) >> 5) + 1) : nblk;
 
-    f32x16_t oacc[ND], lacc;  // lacc row 0: sum of the rounded P
-    float lrow;  // this lane's share (16 of each block's 32 keys) of the unrounded P's sum
+    f32x16_t oacc[ND];
+    // this lane's share (16 of each block's 32 keys) of the sums of the
+    // rounded P (normalises O) and of the unrounded P (gives L)
+    float lrnd, lrow;
     float m_run;
-    // P = exp2(c S - m) for one block, then O^T += V^T P^T and l_r += 1^T P^T
+    // P = exp2(c S - m) for one block, then O^T += V^T P^T and l_r += sum P
     // (P rounded to the element type) and l += sum P (fp32, unrounded)
     auto pv = [&](const f32x16_t& s, float moff, frag (*vA)[2]) {
       frag pf[2];
@@ -285,18 +291,19 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
         pe[i] = fast_exp2(fmaf(s[i], c, -moff));
         pf[i >> 3][i & 7] = (T)pe[i];
       }
-      if constexpr (SOFTMAX) lrow += tree_sum16(pe);
+      if constexpr (SOFTMAX) {
+        lrow += tree_sum16(pe);
+        lrnd += dot8<T>(pf[0], ones) + dot8<T>(pf[1], ones);
+      }
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int d = 0; d < ND; ++d) oacc[d] = E::mma(vA[d][t], pf[t], oacc[d]);
-        if constexpr (SOFTMAX) lacc = E::mma(onesA, pf[t], lacc);
-      }
     };
     auto init = [&](float m0) {
 #pragma unroll
       for (int d = 0; d < ND; ++d) oacc[d] = zero16();
-      lacc = zero16();
+      lrnd = 0.f;
       lrow = 0.f;
       m_run = m0;
     };
@@ -319,7 +326,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
             const float alpha = (mnew == -__builtin_inff()) ? 1.f : fast_exp2(m_run - mnew);
 #pragma unroll
             for (int d = 0; d < ND; ++d) oacc[d] *= alpha;
-            lacc *= alpha;
+            lrnd *= alpha;
             lrow *= alpha;
             m_run = mnew;
           }
@@ -356,12 +363,14 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
     };
 
     constexpr bool STATIC = SOFTMAX && !std::is_same<T, _Float16>::value;
-    if (!(SOFTMAX && !STATIC) && npre == 0) {
+    constexpr bool PIPE = W <= 12;  // registers for the pipelined key loop
+    if (PIPE && !(SOFTMAX && !STATIC) && npre == 0) {
       run_fixed();
     } else if constexpr (SOFTMAX && !STATIC) {
       run_safe();
     } else {
-      // fixed offset with a num_prefix mask: the generic loop at the fixed offset
+      // fixed offset with a num_prefix mask, or 16 waves: the plain loop at
+      // the fixed offset
       init(SOFTMAX ? qn2 - kBoundMargin : qn2);
       for (int kb = 0; kb < kend; ++kb) {
         const int k0 = org + 32 * kb;
@@ -380,7 +389,7 @@ __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
     }
 
     const float lsum = SOFTMAX ? xhalf_sum(lrow) : 1.f;
-    const float inv = SOFTMAX ? 1.f / xhalf_sum(lacc[0]) : 1.f;
+    const float inv = SOFTMAX ? 1.f / xhalf_sum(lrnd) : 1.f;
     if (qvalid) {
       T* orow = O + (int64_t)qtok * p.so[2];
 #pragma unroll

@@ -872,12 +872,11 @@ __device__ inline f32x16_t splat16(float x) {
 //   P   = exp2(c S^T - m),
 //   O^T += V^T P^T with P rounded to the element type (as the reference
 //   rounds it before its P V product, rbf_attention.py:201),
-//   l_r += the rounded P's sum, in fp32 (this streaming forward: v_dot2
-//   against ones on the VALU, 2 MFMAs per block fewer, C3 forward 1140 ->
-//   1128 us; the head-resident forward: 1^T P^T on the MFMA path, through an
-//   operand whose first row is ones): O is normalised by the sum of exactly
-//   the rounded P its numerator uses, so a row that sees one key returns that
-//   key's v exactly;
+//   l_r += the rounded P's sum, in fp32 (v_dot2 against ones on the VALU, 2
+//   MFMAs per block fewer than a ones-row product, C3 forward 1140 ->
+//   1128 us; the head-resident forward does the same): O is normalised by
+//   the sum of exactly the rounded P its numerator uses, so a row that sees
+//   one key returns that key's v exactly;
 //   l += sum_j P in fp32 from the unrounded P, for L (the reference sums the
 //   unrounded P, 196-198).  L taken from l_r was off by up to 2^-9 relative
 //   per row, a scale every P of the backward then carried (dV's error at
@@ -891,11 +890,10 @@ __device__ inline f32x16_t splat16(float x) {
 // cannot hold P up to 2^60 and always takes the online max.
 // ---------------------------------------------------------------------------
 template <typename T>
-__device__ inline typename Elem<T>::frag ones_row_frag(int n) {
+__device__ inline typename Elem<T>::frag ones_frag() {
   typename Elem<T>::frag f;
-  const T v = (T)(n == 0 ? 1.f : 0.f);
 #pragma unroll
-  for (int s = 0; s < 8; ++s) f[s] = v;
+  for (int s = 0; s < 8; ++s) f[s] = (T)1.f;
   return f;
 }
 

@@ -233,12 +233,12 @@ template <int DP, bool SM>
 hipError_t fwd_default(const Params& p, hipStream_t st) {
   if (p.pos) {
     if constexpr (!kIsF32 && DP == 64) {
-      if (p.nblk <= kHrBlocks64) return hr_fwd(p, SM, 12, st);
+      if (p.nblk <= kHrBlocks64) return hr_fwd(p, SM, 0, st);
     }
     return hipErrorInvalidValue;
   }
   if constexpr (!kIsF32 && DP == 64) {
-    if (use_hr(p, kHrBlocks64, 1)) return hr_fwd(p, SM, 12, st);
+    if (use_hr(p, kHrBlocks64, 1)) return hr_fwd(p, SM, 0, st);
   }
   if constexpr (kIsF32) return fwd_cfg<DP, SM, 4, 32>(p, st);
   else if constexpr (DP == 256) {
@@ -371,7 +371,7 @@ hipError_t fwd_any_cfg(const Params& p, hipStream_t st) {
       if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return hr_fwd(p, SM, 8, st); }
       break;
     case 11:
-      if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return hr_fwd(p, SM, 12, st); }
+      if constexpr (DP == 64) { if (p.nblk <= kHrBlocks64) return hr_fwd(p, SM, 0, st); }
       break;
     default: break;
   }

@@ -63,8 +63,9 @@ bool fits(const Params& p) { return p.D > 32 && p.D <= DP && p.nblk <= NB; }
 #define RBF_CAT2(a, b) a##b
 #define RBF_CAT(a, b) RBF_CAT2(a, b)
 
-// waves: 12 (default) or 8 (a tuning alternative, softmax without a position
-// term; the softmax forward with a position term always runs 8).
+// waves: 8 selects the 8-wave softmax forward (a tuning alternative, without
+// a position term); any other value the default: softmax 16 waves,
+// non-softmax 12, softmax with a position term 8.
 hipError_t RBF_CAT(launch_fwd_hr_, RBF_NAME)(const Params& p, int variant, int waves, hipStream_t st) {
   if (!fits(p)) return hipErrorInvalidValue;
   const bool sm = variant == 0;
@@ -73,7 +74,7 @@ hipError_t RBF_CAT(launch_fwd_hr_, RBF_NAME)(const Params& p, int variant, int w
   // together): 8 waves, measured as fast as 12 with spills.
   if (p.pos) return sm ? fwd_cfg<true, 8, true>(p, st) : fwd_cfg<false, 12, true>(p, st);
   if (waves == 8 && sm) return fwd_cfg<true, 8, false>(p, st);
-  return sm ? fwd_cfg<true, 12, false>(p, st) : fwd_cfg<false, 12, false>(p, st);
+  return sm ? fwd_cfg<true, 16, false>(p, st) : fwd_cfg<false, 12, false>(p, st);
 }
 
 hipError_t RBF_CAT(launch_bwd_dq_hr_, RBF_NAME)(const Params& p, int variant, hipStream_t st) {
