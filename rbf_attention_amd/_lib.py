@@ -188,18 +188,20 @@ def load(path: str | None = None):
 
 
 def tensor_desc(t: torch.Tensor | None) -> Tensor:
+    """Descriptor of a (B, H, N, D) tensor.  The stride of a dimension of
+    size 1 is never used (its only index is 0) and is passed as 0, so that
+    torch's arbitrary strides for such dimensions pass the alignment check."""
     if t is None:
         return Tensor(None, 0, 0, 0)
-    s = t.stride()
-    return Tensor(t.data_ptr(), s[0], s[1], s[2])
+    s, n = t.stride(), t.shape
+    return Tensor(t.data_ptr(), s[0] if n[0] != 1 else 0, s[1] if n[1] != 1 else 0, s[2] if n[2] != 1 else 0)
 
 
 def pos_desc(pos: torch.Tensor) -> PosTerm:
     """Descriptor of a (1 or B, H, N, D) position term; a batch-1 term is
     passed with stride_b = 0, as the library requires (it reads it at every b)."""
-    s = pos.stride()
     batch = pos.shape[0]
-    return PosTerm(Tensor(pos.data_ptr(), 0 if batch == 1 else s[0], s[1], s[2]), batch)
+    return PosTerm(tensor_desc(pos), batch)
 
 
 def decode_workspace_size(args: DecodeArgs) -> int:
@@ -211,7 +213,7 @@ def decode_workspace_size(args: DecodeArgs) -> int:
 
 
 def call(fn_name: str, args, stream: int, *extra: int) -> None:
-    lib = load()
+    lib = _lib if _lib is not None else load()
     rc = getattr(lib, fn_name)(ctypes.byref(args), ctypes.c_void_p(stream), *extra)
     if rc != 0:
         msg = lib.rbf_attn_last_error().decode(errors="replace")

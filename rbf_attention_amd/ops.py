@@ -31,6 +31,7 @@ import math
 from typing import Optional
 
 import torch
+import torch.utils._python_dispatch as _python_dispatch
 
 from . import _lib
 
@@ -73,6 +74,8 @@ def _prep(t: torch.Tensor, dpad: int) -> torch.Tensor:
     d = t.shape[-1]
     if dpad != d:
         return torch.nn.functional.pad(t, (0, dpad - d))
+    if t.is_contiguous() and t.data_ptr() % 16 == 0:
+        return t  # strides are multiples of d, a multiple of 8 elements
     esz = t.element_size()
     ok = (
         t.stride(-1) == 1
@@ -95,18 +98,26 @@ def _base_args(variant: int, q: torch.Tensor, is_causal: bool, sm_scale: float, 
     return a
 
 
+def _stream(device: torch.device) -> int:
+    """The current stream of the tensors' device (raw handle)."""
+    return torch._C._cuda_getCurrentRawStream(device.index)
+
+
 def _launch(fn: str, a, device: torch.device) -> None:
     if a.B * a.H * a.N == 0:
         return  # empty problem: nothing to compute (data pointers may be NULL)
-    with torch.cuda.device(device):
-        _lib.call(fn, a, torch.cuda.current_stream(device).cuda_stream)
+    if torch.cuda.current_device() == device.index:
+        _lib.call(fn, a, _stream(device))
+    else:
+        with torch.cuda.device(device):
+            _lib.call(fn, a, _stream(device))
 
 
 def _launch_pos(fn: str, a, pos: torch.Tensor, device: torch.device) -> None:
     if a.B * a.H * a.N == 0:
         return
     with torch.cuda.device(device):
-        _lib.call_pos(fn, a, _lib.pos_desc(pos), torch.cuda.current_stream(device).cuda_stream)
+        _lib.call_pos(fn, a, _lib.pos_desc(pos), _stream(device))
 
 
 def _check_pos(name: str, q: torch.Tensor, pos: torch.Tensor) -> None:
@@ -565,6 +576,49 @@ def rbf_decode(q, k_cache, v_cache, cache_lens=None, *, softmax=True, sm_scale=N
 # ---------------------------------------------------------------------------
 # Public wrappers (rbf_attention.py:848-853) and autograd.Function aliases.
 # ---------------------------------------------------------------------------
+class _EagerRbfAttention(torch.autograd.Function):
+    """The wrappers' eager path: the ops' kernels and autograd formula (same
+    implementations, so bit-identical results) without the torch.library
+    dispatch, whose Python layers cost ~140 us of host time per forward +
+    backward (MI355X box: 213 us through ``rbf_attn_v5::scaled_fwd`` and its
+    registered autograd against 73 us this way, tiny shapes)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, pos, softmax, is_causal, scale, num_prefix, token_major):
+        if softmax:
+            out, L = _softmax_fwd(q, k, v, is_causal, scale, num_prefix, token_major, pos)
+            ctx.save_for_backward(q, k, v, out, L, pos)
+        else:
+            out = _non_softmax_fwd(q, k, v, is_causal, scale, num_prefix, token_major, pos)
+            ctx.save_for_backward(q, k, v, pos)
+        ctx.cfg = (softmax, is_causal, scale, num_prefix)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        softmax, is_causal, scale, num_prefix = ctx.cfg
+        if softmax:
+            q, k, v, out, L, pos = ctx.saved_tensors
+            dq, dk, dv = _softmax_bwd(q, k, v, out, L, dout, is_causal, scale, num_prefix, pos)
+        else:
+            q, k, v, pos = ctx.saved_tensors
+            dq, dk, dv = _non_softmax_bwd(q, k, v, dout, is_causal, scale, num_prefix, pos)
+        return dq, dk, dv, _pos_grad(pos, dq, dk), None, None, None, None, None
+
+
+def _eager_plain(*ts) -> bool:
+    """Whether a wrapper call may take the eager path: plain GPU tensors (no
+    subclass: fake, functional, distributed ...; no meta or CPU tensors), not
+    under torch.compile / export tracing, no dispatch mode and no functorch
+    transform.  Everything else goes through the registered ops, which those
+    mechanisms know (and which raise for CPU tensors)."""
+    if torch.compiler.is_compiling() or torch._C._are_functorch_transforms_active():
+        return False
+    if _python_dispatch._get_current_dispatch_mode() is not None:
+        return False
+    return all(t is None or (type(t) is torch.Tensor and t.is_cuda) for t in ts)
+
+
 def run_triton_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, token_major=False, pos=None):
     """Softmax RBF attention.  With the default ``sm_scale`` (1/sqrt(D)),
     ``num_prefix=0``, ``token_major=False`` and no ``pos`` this is exactly the
@@ -572,7 +626,12 @@ def run_triton_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, toke
     (B, H, N, D) output as a view of a (B, N, H, D) buffer (see
     ``_alloc_out``).  ``pos`` (1 or B, H, N, D): attention of q + pos and
     k + pos (the model's SuSiE embedding), fused into the kernels' Q/K reads
-    where the library supports it; its gradient is returned by autograd."""
+    where the library supports it; its gradient is returned by autograd.
+    Eager calls on plain tensors run the ops' implementations directly
+    (``_EagerRbfAttention``); traced and transformed calls run the ops."""
+    if _eager_plain(q, k, v, pos):
+        scale = _default_scale(q) if sm_scale is None else float(sm_scale)
+        return _EagerRbfAttention.apply(q, k, v, pos, True, bool(is_causal), scale, int(num_prefix), bool(token_major))
     if sm_scale is None and num_prefix == 0 and not token_major and pos is None:
         return torch.ops.rbf_attn_v5.scaled_fwd(q, k, v, is_causal)[0]
     scale = _default_scale(q) if sm_scale is None else float(sm_scale)
@@ -580,8 +639,11 @@ def run_triton_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, toke
 
 
 def run_triton_non_softmax_rbf(q, k, v, is_causal=True, *, sm_scale=None, num_prefix=0, token_major=False, pos=None):
-    """Non-softmax RBF attention, sum_j exp(-gamma||q_i-k_j||^2) v_j (pos as
-    in ``run_triton_rbf``)."""
+    """Non-softmax RBF attention, sum_j exp(-gamma||q_i-k_j||^2) v_j (pos and
+    the eager path as in ``run_triton_rbf``)."""
+    if _eager_plain(q, k, v, pos):
+        scale = _default_scale(q) if sm_scale is None else float(sm_scale)
+        return _EagerRbfAttention.apply(q, k, v, pos, False, bool(is_causal), scale, int(num_prefix), bool(token_major))
     if sm_scale is None and num_prefix == 0 and not token_major and pos is None:
         return torch.ops.rbf_attn_v5.non_softmax_fwd(q, k, v, is_causal)
     scale = _default_scale(q) if sm_scale is None else float(sm_scale)

@@ -564,6 +564,55 @@ def test_autograd_function_aliases(cuda_device):
         assert torch.equal(x, y)
 
 
+@pytest.mark.parametrize("softmax", [True, False])
+@pytest.mark.parametrize("opts", ["reference", "extended"])
+def test_eager_wrappers_equal_registered_ops(cuda_device, softmax, opts):
+    """Eager run_triton_rbf / run_triton_non_softmax_rbf take an
+    autograd.Function over the ops' implementations instead of the
+    torch.library dispatch; output (values and strides) and every gradient,
+    the position term's included, must equal the registered ops' bit for bit."""
+    q, k, v, do = rand_inputs(2, 4, 130, 64, torch.bfloat16, cuda_device, std=1.0 if softmax else 0.5, seed=7)
+    P = (torch.randn(1, 4, 130, 64, generator=torch.Generator().manual_seed(8)) * 0.3).to(torch.bfloat16).to(cuda_device)
+    ext = opts == "extended"
+    fn = ra.run_triton_rbf if softmax else ra.run_triton_non_softmax_rbf
+    if ext:
+        kw = dict(sm_scale=0.0625, num_prefix=4, token_major=True)
+        op = torch.ops.rbf_attn_amd.scaled_fwd_ex if softmax else torch.ops.rbf_attn_amd.non_softmax_fwd_ex
+        call_op = lambda a, b, c, p: op(a, b, c, True, 0.0625, 4, True, p)
+    else:
+        kw = {}
+        op = torch.ops.rbf_attn_v5.scaled_fwd if softmax else torch.ops.rbf_attn_v5.non_softmax_fwd
+        call_op = lambda a, b, c, p: op(a, b, c, True)
+    results = []
+    for path in ("eager", "op"):
+        leaves = [t.clone().requires_grad_(True) for t in (q, k, v)] + ([P.clone().requires_grad_(True)] if ext else [])
+        pos = leaves[3] if ext else None
+        if path == "eager":
+            out = fn(leaves[0], leaves[1], leaves[2], True, pos=pos, **kw)
+            assert type(out.grad_fn).__name__ == "_EagerRbfAttentionBackward"
+        else:
+            out = call_op(leaves[0], leaves[1], leaves[2], pos)
+            out = out[0] if softmax else out
+            assert type(out.grad_fn).__name__ != "_EagerRbfAttentionBackward"
+        out.backward(do)
+        torch.cuda.synchronize()
+        results.append([out.detach()] + [t.grad for t in leaves])
+    for i, (x, y) in enumerate(zip(*results)):
+        assert x.shape == y.shape and x.stride() == y.stride(), (i, x.stride(), y.stride())
+        assert torch.equal(x, y), f"tensor {i}: max diff {(x.float() - y.float()).abs().max().item():.3e}"
+
+
+def test_size_one_dims_take_any_stride(cuda_device):
+    """torch gives a dimension of size 1 an arbitrary stride (the tensor still
+    counts as contiguous); such a stride is never used and must not trip the
+    C ABI's 16-byte stride check."""
+    q, k, v, do = rand_inputs(1, 2, 70, 64, torch.bfloat16, cuda_device, seed=9)
+    odd = [t.as_strided(t.shape, (3,) + t.stride()[1:]) for t in (q, k, v)]
+    assert all(t.is_contiguous() for t in odd)
+    for fn in (ra.run_triton_rbf, ra.run_triton_non_softmax_rbf):
+        assert torch.equal(fn(*odd, True), fn(q, k, v, True))
+
+
 def test_empty_batch(cuda_device):
     q = torch.zeros(0, 2, 16, 64, device=cuda_device, dtype=torch.bfloat16)
     out = ra.run_triton_rbf(q, q, q)
