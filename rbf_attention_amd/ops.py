@@ -103,14 +103,20 @@ def _stream(device: torch.device) -> int:
     return torch._C._cuda_getCurrentRawStream(device.index)
 
 
-def _launch(fn: str, a, device: torch.device) -> None:
-    if a.B * a.H * a.N == 0:
-        return  # empty problem: nothing to compute (data pointers may be NULL)
+def _call_on(device: torch.device, fn: str, a) -> None:
+    """One C-ABI call on the current stream of `device`, with that device
+    current during the call."""
     if torch.cuda.current_device() == device.index:
         _lib.call(fn, a, _stream(device))
     else:
         with torch.cuda.device(device):
             _lib.call(fn, a, _stream(device))
+
+
+def _launch(fn: str, a, device: torch.device) -> None:
+    if a.B * a.H * a.N == 0:
+        return  # empty problem: nothing to compute (data pointers may be NULL)
+    _call_on(device, fn, a)
 
 
 def _launch_pos(fn: str, a, pos: torch.Tensor, device: torch.device) -> None:
@@ -537,8 +543,7 @@ def _decode(q, k_cache, v_cache, cache_lens, softmax: bool, sm_scale: float):
     ws = torch.empty((nbytes + 15) // 16 * 4, device=q.device, dtype=torch.float32)
     a.workspace = ws.data_ptr()
     a.workspace_bytes = nbytes
-    with torch.cuda.device(q.device):
-        _lib.call("rbf_attn_decode", a, torch.cuda.current_stream(q.device).cuda_stream)
+    _call_on(q.device, "rbf_attn_decode", a)
     return _unpad(out, D), lse
 
 
@@ -570,6 +575,8 @@ def rbf_decode(q, k_cache, v_cache, cache_lens=None, *, softmax=True, sm_scale=N
     the base-2 log-sum-exp (softmax; unspecified for the non-softmax variant).
     Forward only."""
     scale = _default_scale(q) if sm_scale is None else float(sm_scale)
+    if _eager_plain(q, k_cache, v_cache) and (cache_lens is None or type(cache_lens) is torch.Tensor):
+        return _decode(q, k_cache, v_cache, cache_lens, bool(softmax), scale)  # the op's implementation
     return torch.ops.rbf_attn_amd.decode(q, k_cache, v_cache, cache_lens, bool(softmax), scale)
 
 

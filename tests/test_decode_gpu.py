@@ -87,6 +87,21 @@ def test_decode_equals_last_rows_of_forward(cuda_device):
     assert (lse - L).abs().max().item() <= 2e-2
 
 
+@pytest.mark.parametrize("softmax", [True, False])
+def test_decode_wrapper_equals_registered_op(cuda_device, softmax):
+    """Eager rbf_decode on plain GPU tensors calls the op's implementation
+    directly; the registered op (rbf_attn_amd::decode) gives the same bits."""
+    q, k, v = make(2, 3, 4, 500, 64, torch.bfloat16, cuda_device, seed=21, std=1.0 if softmax else 0.5)
+    lens = torch.tensor([500, 77], dtype=torch.int32)
+    for lt in (None, lens, lens.to(cuda_device)):
+        out, lse = ra.rbf_decode(q, k, v, lt, softmax=softmax, sm_scale=0.0625)
+        ref, rl = torch.ops.rbf_attn_amd.decode(q, k, v, lt, softmax, 0.0625)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        if softmax:
+            assert torch.equal(lse, rl)
+
+
 def test_decode_strided_cache_views(cuda_device):
     """Caches as head-interleaved views of one (B, L, H, D) buffer."""
     B, H, L, D, T = 2, 4, 600, 64, 2

@@ -600,6 +600,11 @@ def test_eager_wrappers_equal_registered_ops(cuda_device, softmax, opts):
     for i, (x, y) in enumerate(zip(*results)):
         assert x.shape == y.shape and x.stride() == y.stride(), (i, x.stride(), y.stride())
         assert torch.equal(x, y), f"tensor {i}: max diff {(x.float() - y.float()).abs().max().item():.3e}"
+    # without autograd recording: no_grad and inference mode give the same output
+    for ctx in (torch.no_grad, torch.inference_mode):
+        with ctx():
+            out = fn(q, k, v, True, pos=P if ext else None, **kw)
+        assert out.grad_fn is None and torch.equal(out, results[0][0])
 
 
 def test_size_one_dims_take_any_stride(cuda_device):
