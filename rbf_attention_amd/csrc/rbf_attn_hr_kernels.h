@@ -186,15 +186,16 @@ __device__ inline int hr_block(int k, int wave, int W, int nblk, bool reverse) {
 // or as a per-block rerun when a row's sum leaves [2^-60, 2^100]), reading K
 // rows and transposed V from the resident tiles.
 //
-// With up to 12 waves and no running max (non-softmax) the key loop is
-// software pipelined: iteration kb issues the S MFMAs of block kb+1 (K
-// fragments and norms read one block earlier) next to the exponentials of
-// block kb, so the MFMA and VALU work of one wave overlap.  Only the causal
-// diagonal block needs a mask; it is peeled off the loop.  The softmax forward
-// runs 16 waves (4 per SIMD) with the plain loop instead: its registers fit
-// 128 per lane only without the pipeline's second S accumulator and norm rows,
-// and the other waves on the SIMD do the overlapping (C2 forward 22.9 -> 22.4
-// us against 12 pipelined waves; fp16 24.1 -> 23.5).
+// With up to 12 waves and no running max (the static softmax bound,
+// non-softmax) the key loop is software pipelined: iteration kb issues the S
+// MFMAs of block kb+1 (K fragments and norms read one block earlier) next to
+// the exponentials of block kb, so the MFMA and VALU work of one wave overlap.
+// Only the causal diagonal block needs a mask; it is peeled off the loop.  The
+// softmax forward without a position term runs 16 waves (4 per SIMD) with the
+// plain loop instead: its registers fit 128 per lane only without the
+// pipeline's second S accumulator and norm rows, and the other waves on the
+// SIMD do the overlapping (C2 forward 22.9 -> 22.4 us against 12 pipelined
+// waves; fp16 24.1 -> 23.5).
 // ---------------------------------------------------------------------------
 template <typename T, int DP, int W, int NB, bool SOFTMAX, bool POS = false>
 __global__ __launch_bounds__(64 * W) void rbf_fwd_hr_kernel(const Params p) {
