@@ -66,3 +66,32 @@ def test_shape_and_dtype_checks():
 def test_public_surface():
     for name in ("run_triton_rbf", "run_triton_non_softmax_rbf", "TritonRBFAttention", "TritonNonSoftmaxRBFAttention"):
         assert hasattr(ra, name)
+
+
+def test_eager_path_predicate():
+    """The wrappers take their eager autograd.Function path only for plain GPU
+    tensors outside tracing, dispatch modes and functorch transforms; CPU and
+    meta tensors, tensor subclasses and active dispatch modes go through the
+    registered ops (which refuse CPU tensors and trace meta ones)."""
+    from torch.utils._python_dispatch import TorchDispatchMode
+    from rbf_attention_amd import ops
+
+    cpu = torch.randn(1, 1, 8, 64)
+    assert not ops._eager_plain(cpu, cpu, cpu, None)
+    m = meta(1, 1, 8, 64)
+    assert not ops._eager_plain(m, m, m, None)
+
+    class Sub(torch.Tensor):
+        pass
+
+    assert not ops._eager_plain(cpu.as_subclass(Sub), cpu, cpu, None)
+
+    class Mode(TorchDispatchMode):
+        def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+            return func(*args, **(kwargs or {}))
+
+    with Mode():
+        assert not ops._eager_plain(cpu, cpu, cpu, None)
+    # the meta tensors go through the ops' fake implementations
+    assert ra.run_triton_rbf(m, m, m).shape == m.shape
+    assert ra.run_triton_non_softmax_rbf(m, m, m, sm_scale=0.1, num_prefix=2).shape == m.shape
